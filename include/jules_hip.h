@@ -1,0 +1,204 @@
+/*
+ * jules_hip.h - C ABI of the MI355X (gfx950) kernel library libjules_hip.so.
+ *
+ * This is the drop-in boundary for the Jules kernel path.  In the reference
+ * the path is a set of header-defined C++ functions in namespace
+ * jules::kernel (include/jules/Kernel/FusedKernels.h, FlashAttention.h) plus
+ * the kernel-name strings that KernelRoutingPass writes into
+ * jules.extern_kernel / stablehlo.custom_call ops.  This header replaces both:
+ *
+ *   - typed entry points (device pointers, an explicit hipStream_t passed as
+ *     void*, an int status) for each kernel, and
+ *   - a name registry, jules_hip_lookup(), that resolves the extern_kernel /
+ *     custom_call target names to a uniform descriptor-based calling
+ *     convention (what a ROCm PJRT device or an ORC symbol resolver binds).
+ *
+ * The C++ signatures of jules::kernel themselves (host buffers, synchronous)
+ * are provided by jules_hip_kernel.hpp on top of this ABI.
+ *
+ * Conventions
+ *   - All tensors are dense row-major in device memory (hipMalloc'd or any
+ *     pointer the device can access).  Shapes use int like the reference.
+ *   - Every entry point validates its arguments and returns a jh_status; no
+ *     entry point aborts.  A non-zero status leaves outputs unspecified
+ *     (argument errors are detected before any launch and write nothing).
+ *     jules_hip_last_error() returns a thread-local message for the last
+ *     failure on the calling thread.
+ *   - Launches are asynchronous on `stream` (NULL = the legacy default
+ *     stream).  Entry points are re-entrant; calls on different streams may
+ *     overlap.  Buffers passed to one call must not be written concurrently.
+ *   - Activation codes keep jules::kernel::ActivationType's values
+ *     (reference FusedKernels.h:61-67) and add SiLU = 5.
+ *   - bf16 is IEEE bfloat16 (uint16 bit pattern), rounded to nearest even.
+ */
+#ifndef JULES_HIP_H
+#define JULES_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JULES_HIP_ABI_VERSION 1
+
+typedef enum jh_status {
+    JH_OK = 0,
+    JH_ERR_NULL = 1,        /* a required pointer is NULL */
+    JH_ERR_SHAPE = 2,       /* negative, zero-where-forbidden or too large dimension */
+    JH_ERR_DTYPE = 3,       /* dtype not supported by this entry point */
+    JH_ERR_ALIGN = 4,       /* pointer misaligned for the required vector width */
+    JH_ERR_ACT = 5,         /* unknown activation code */
+    JH_ERR_WORKSPACE = 6,   /* workspace NULL or smaller than required */
+    JH_ERR_HIP = 7,         /* the HIP runtime reported an error */
+    JH_ERR_UNSUPPORTED = 8, /* valid request this build does not implement */
+    JH_ERR_NOT_FOUND = 9,   /* registry: unknown kernel name */
+    JH_ERR_ARG = 10         /* any other invalid argument (scale, rank, ...) */
+} jh_status;
+
+typedef enum jh_dtype {
+    JH_F32 = 0,
+    JH_BF16 = 1,
+    JH_I8 = 2,
+    JH_I32 = 3
+} jh_dtype;
+
+typedef enum jh_act {
+    JH_ACT_NONE = 0,
+    JH_ACT_RELU = 1,
+    JH_ACT_SIGMOID = 2,
+    JH_ACT_TANH = 3,
+    JH_ACT_GELU = 4, /* tanh approximation, reference FusedKernels.h:155-164 */
+    JH_ACT_SILU = 5  /* x * sigmoid(x); no reference counterpart */
+} jh_act;
+
+/* ---- library information ------------------------------------------------ */
+int jules_hip_abi_version(void);
+const char* jules_hip_status_string(int status);
+const char* jules_hip_last_error(void);
+
+/* ---- fused GEMM + bias + activation --------------------------------------
+ * C[M,N] = act(A[M,K] . B[K,N] + bias[N])
+ *
+ * Replaces (reference include/jules/Kernel/FusedKernels.h):
+ *   tiledMatmulWithActivation(A,B,C,M,N,K,cfg,act)  :378   (bias = NULL)
+ *   fusedMatmulBiasRelu(X,W,bias,out,M,K,N)         :265   (act = RELU)
+ *   fusedMatmulRelu(X,W,out,M,K,N)                  :203   (bias = NULL, act = RELU)
+ * and the routed names fusedMatmul<Act> / fusedMatmulBias<Act>
+ * (lib/Passes/KernelRoutingPass.cpp:144-166, :189-211).
+ *
+ * dtype JH_F32: A, B, C float.  Each C[i,j] is the sequential fma chain
+ *   over k = 0..K-1 starting from 0, then + bias[j], then the activation of
+ *   the reference's vector path (fast_exp based, FusedKernels.h:90-164), so
+ *   results equal the reference AVX-512 kernel bit for bit whenever its
+ *   vector path covers the column (N and tile_n multiples of 16).
+ * dtype JH_BF16: A, B, C bf16; fp32 accumulation on MFMA; bias fp32;
+ *   epilogue in fp32, C rounded to bf16.  M, N, K must be multiples of 8
+ *   (16-byte rows); other shapes return JH_ERR_UNSUPPORTED.
+ * bias may be NULL.  K = 0 gives act(bias) (act(0) without bias).
+ */
+int jules_hip_gemm_bias_act(int dtype, int act, const void* A, const void* B,
+                            const float* bias, void* C, int M, int N, int K,
+                            void* stream);
+
+/* ---- elementwise activation ----------------------------------------------
+ * out[i] = act(in[i]), fp32, n elements.  act = GELU replaces
+ * fusedGelu(out,in,N) (reference FusedKernels.h:606) and the routed name
+ * "fusedGelu" (KernelRoutingPass.cpp:287).  In-place (out == in) is allowed.
+ */
+int jules_hip_activation(int act, float* out, const float* in, int64_t n,
+                         void* stream);
+
+/* ---- flash-attention forward ---------------------------------------------
+ * O = softmax(scale * Q K^T [+ causal mask]) V, per (b,h); Q,K,V,O [B,H,S,D].
+ *
+ * Replaces flashAttention(out,Q,K,V,B,H,S,D,arena,planner) and
+ * attention(...) (reference include/jules/Kernel/FlashAttention.h:130, :114),
+ * which are non-causal with scale fixed at 1/sqrtf(D) (:135); causal = 1
+ * excludes keys j > query i.
+ * dtype JH_F32 or JH_BF16 (Q, K, V, O share it); softmax statistics are fp32.
+ * D must be 64 or 128.  S >= 1.  scale must be finite and > 0.
+ * lse (optional, fp32 [B,H,S]) receives the natural-log log-sum-exp of the
+ * scaled, masked scores of each row.
+ */
+int jules_hip_flash_attn_fwd(int dtype, int causal, float scale,
+                             const void* Q, const void* K, const void* V,
+                             void* O, float* lse, int B, int H, int S, int D,
+                             void* stream);
+
+/* ---- W8A16 decode GEMM + bias + activation --------------------------------
+ * y[m,j] = act(scale[j] * sum_k x[m,k] * W[k,j] + bias[j])
+ * x bf16 [M,K], W int8 [K,N] (row-major, indexed W[k*N+j] like matmulInt8,
+ * reference FusedKernels.h:1053), scale fp32 [N] per output channel, bias
+ * fp32 [N] or NULL, y bf16 [M,N].  fp32 accumulation; the int8 -> fp32
+ * dequantisation is exact.  Deterministic: the split-K reduction sums the
+ * partials in a fixed order.
+ * Constraints: 1 <= M <= 16, N % 16 == 0, K % 2 == 0, W 16-byte aligned.
+ * workspace: device memory of at least jules_hip_w8a16_workspace_size(M,N,K)
+ * bytes, zero-filled before its first use; the kernel leaves it zeroed again
+ * (counters are reset by the last block), so one workspace can serve any
+ * number of sequential calls on one stream.  Calls that overlap in time need
+ * separate workspaces.
+ * No reference counterpart: the reference's int8 kernel (matmulInt8,
+ * FusedKernels.h:867) is W8A8 with one scalar scale; routed name
+ * "matmulW8A16BiasSilu" is new.
+ */
+size_t jules_hip_w8a16_workspace_size(int M, int N, int K);
+int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W,
+                                  const float* scale, const float* bias,
+                                  void* y, int M, int N, int K,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/* ---- int8 x int8 GEMM (matmulInt8 semantics) -------------------------------
+ * C[i,j] = float(sum_k A[i,k]*B[k,j]) * (scale_A*scale_B) [+ bias[j]]
+ * Replaces matmulInt8(A,B,C,M,N,K,scale_A,scale_B,bias,arena) with the
+ * semantics of its scalar path (reference FusedKernels.h:1046-1066): exact
+ * int32 accumulation, B indexed B[k*N+j]; the product scale_A*scale_B is
+ * rounded to fp32 first, then one multiply, then one add of bias.
+ * (The reference's AVX-512F and VNNI paths index the wrong columns; this
+ * entry point follows the scalar path.)  K <= 131072 keeps int32 exact.
+ */
+int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M,
+                          int N, int K, float scale_A, float scale_B,
+                          const float* bias, void* stream);
+
+/* ---- kernel-name registry -------------------------------------------------
+ * Resolves the names KernelRoutingPass emits (fusedMatmul{Relu,Sigmoid,Tanh,
+ * Gelu}, fusedMatmulBias{Relu,Sigmoid,Tanh,Gelu}, fusedGelu, matmulInt8,
+ * flashAttention) and the ones this library adds (fusedMatmul,
+ * fusedMatmulBias, fusedMatmulBiasSilu, flashAttentionCausal,
+ * matmulW8A16BiasSilu) to a descriptor-based entry point.  The descriptor
+ * extends the reference's TensorDescriptor (include/jules/LLVMBackend.h:60-66:
+ * data, offset, sizes[6], strides[6], rank) with a dtype; data + offset is
+ * the device address of element 0 and strides are in elements.
+ * Operand order follows extern_kernel: (lhs, rhs[, bias]) for the matmuls
+ * (KernelRoutingPass.cpp:154,198), (Q, K, V) for attention,
+ * (x, W, scale[, bias]) for W8A16, (A, B[, bias]) plus backend_config
+ * "scale_a=<f>,scale_b=<f>" for matmulInt8 (the reference emits no scales,
+ * KernelRoutingPass.cpp:406-410).  Attention accepts backend_config
+ * "scale=<f>"; the default is 1/sqrtf(D).  W8A16 needs a workspace; its
+ * registry entry allocates one per device on first use.
+ */
+typedef struct jh_tensor {
+    void* data;
+    int64_t offset;
+    int64_t sizes[6];
+    int64_t strides[6];
+    int32_t rank;
+    int32_t dtype; /* jh_dtype */
+} jh_tensor;
+
+typedef int (*jh_kernel_fn)(int n_inputs, const jh_tensor* inputs,
+                            int n_outputs, jh_tensor* outputs,
+                            const char* backend_config, void* stream);
+
+jh_kernel_fn jules_hip_lookup(const char* name);
+int jules_hip_kernel_count(void);
+const char* jules_hip_kernel_name(int index);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JULES_HIP_H */

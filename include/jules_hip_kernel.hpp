@@ -1,0 +1,121 @@
+// jules_hip_kernel.hpp - the jules::kernel C++ entry points, on MI355X.
+//
+// Drop-in for the reference's header-defined kernels
+// (include/jules/Kernel/FusedKernels.h, FlashAttention.h, TilePlanner.h,
+// ExecutionArena.h): same namespace, names, argument order and argument
+// meaning, so a caller such as the reference's benchmarks/bench_kernel.cpp
+// switches by including this header instead and linking libjules_hip.so.
+//
+// Like the reference these are synchronous and take caller-owned buffers.
+// Buffers may be host memory (copied to and from the GPU around the call) or
+// device memory (used in place).  The reference returns void and validates
+// nothing; here a failed call leaves the output unspecified and records a
+// jh_status readable with lastStatus() / lastError().  Nothing aborts.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "jules_hip.h"
+
+namespace jules {
+namespace kernel {
+
+// reference FusedKernels.h:61-67; Silu appended (value 5, C ABI JH_ACT_SILU)
+enum class ActivationType { None, Relu, Sigmoid, Tanh, Gelu, Silu };
+
+// reference TilePlanner.h:39-56.  The GPU kernels pick their own tiles; a
+// TileConfig passed in is accepted and does not change results (the
+// reference's results do not depend on it either).
+struct TileConfig {
+    int tile_m;
+    int tile_n;
+    int tile_k;
+    size_t footprintBytes(int M, int N, int K) const;
+    bool fitsInCache(size_t cacheBytes, int M = 0, int N = 0, int K = 0) const;
+};
+
+// reference ExecutionArena.h:41-83, describing the GPU instead of sysfs:
+// l1d = LDS per CU, l2 = L2 per XCD, l3 = last-level (MALL) size.
+struct CacheInfo {
+    size_t l1d_bytes;
+    size_t l2_bytes;
+    size_t l3_bytes;
+    size_t line_bytes;
+    int num_cores;  // compute units
+    static CacheInfo detect();
+};
+
+// reference TilePlanner.h:74-295: a static gfx950 tile table, no timing.
+class TilePlanner {
+public:
+    explicit TilePlanner(const CacheInfo& cache = CacheInfo::detect());
+    TileConfig getTileConfig(int M, int N, int K);
+    TileConfig computeAnalytical(int M, int N, int K) const;
+    void setAutoTune(bool enabled) { autoTune_ = enabled; }
+    void setVerbose(bool v) { verbose_ = v; }
+    const CacheInfo& cacheInfo() const { return cache_; }
+
+private:
+    CacheInfo cache_;
+    bool autoTune_ = true;
+    bool verbose_ = false;
+};
+
+// reference ExecutionArena.h:94-199: bump allocator over one DEVICE buffer
+// (allocated once, 256-byte aligned blocks); reset() frees everything.
+// Overflow returns nullptr and records JH_ERR_WORKSPACE instead of abort().
+class ExecutionArena {
+public:
+    static constexpr size_t DEFAULT_MAX_SIZE = 256UL * 1024 * 1024;
+    explicit ExecutionArena(size_t maxSize = DEFAULT_MAX_SIZE);
+    ~ExecutionArena();
+    ExecutionArena(const ExecutionArena&) = delete;
+    ExecutionArena& operator=(const ExecutionArena&) = delete;
+
+    template <typename T>
+    T* allocate(size_t count) { return static_cast<T*>(allocateBytes(count * sizeof(T))); }
+    void* allocateBytes(size_t bytes);
+    void reset() { offset_ = 0; }
+    void resetAndZero();
+    size_t usedBytes() const { return offset_; }
+    size_t highWaterMark() const { return highWaterMark_; }
+    size_t capacity() const { return maxSize_; }
+    char* rawBuffer() { return buffer_; }
+
+private:
+    char* buffer_ = nullptr;
+    size_t maxSize_ = 0;
+    size_t offset_ = 0;
+    size_t highWaterMark_ = 0;
+};
+
+// status of the last jules::kernel call on this thread (JH_OK on success)
+int lastStatus();
+const char* lastError();
+
+// reference FusedKernels.h:203
+void fusedMatmulRelu(const float* X, const float* W, float* output, int M, int K, int N);
+// reference FusedKernels.h:265
+void fusedMatmulBiasRelu(const float* X, const float* W, const float* bias, float* output, int M,
+                         int K, int N);
+// reference FusedKernels.h:378
+void tiledMatmulWithActivation(const float* A, const float* B, float* C, int M, int N, int K,
+                               const TileConfig& cfg, ActivationType act = ActivationType::None);
+// reference FusedKernels.h:606
+void fusedGelu(float* output, const float* input, int N);
+// reference FusedKernels.h:867 (scalar-path semantics)
+void matmulInt8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K, float scale_A,
+                float scale_B, const float* bias = nullptr, ExecutionArena* arena = nullptr);
+// reference FlashAttention.h:130 (non-causal, scale 1/sqrtf(head_dim))
+void flashAttention(float* output, const float* Q, const float* K, const float* V, int batch,
+                    int heads, int seq, int head_dim, ExecutionArena& arena, TilePlanner& planner);
+// reference FlashAttention.h:114
+void attention(float* output, const float* Q, const float* K, const float* V, int batch,
+               int heads, int seq, int head_dim, ExecutionArena& arena, TilePlanner& planner);
+// reference FlashAttention.h:52 (same result as flashAttention on the GPU)
+void standardAttention(float* output, const float* Q, const float* K, const float* V, int batch,
+                       int heads, int seq, int head_dim, ExecutionArena& arena);
+
+}  // namespace kernel
+}  // namespace jules

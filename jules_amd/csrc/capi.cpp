@@ -1,0 +1,433 @@
+// capi.cpp - the extern "C" boundary of libjules_hip.so (declared in
+// include/jules_hip.h): argument validation, status codes, and the
+// extern_kernel / custom_call name registry.
+//
+// Every entry point checks its arguments before touching the device and
+// returns a jh_status; nothing here aborts (the reference kernels validate
+// nothing and abort() on arena overflow, ExecutionArena.h:140-143).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "jules_hip.h"
+#include "launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return JH_OK;
+    return fail(JH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+bool valid_act(int act) { return act >= JH_ACT_NONE && act <= JH_ACT_SILU; }
+
+// element-count limit: every index is computed in 64-bit, this only guards
+// against sizes whose products overflow int64 in the caller's arithmetic.
+constexpr int64_t kMaxElems = int64_t(1) << 40;
+
+}  // namespace
+
+extern "C" {
+
+int jules_hip_abi_version(void) { return JULES_HIP_ABI_VERSION; }
+
+const char* jules_hip_status_string(int status) {
+    switch (status) {
+    case JH_OK: return "ok";
+    case JH_ERR_NULL: return "null pointer";
+    case JH_ERR_SHAPE: return "invalid shape";
+    case JH_ERR_DTYPE: return "unsupported dtype";
+    case JH_ERR_ALIGN: return "misaligned pointer";
+    case JH_ERR_ACT: return "unknown activation";
+    case JH_ERR_WORKSPACE: return "workspace missing or too small";
+    case JH_ERR_HIP: return "HIP runtime error";
+    case JH_ERR_UNSUPPORTED: return "unsupported configuration";
+    case JH_ERR_NOT_FOUND: return "unknown kernel name";
+    case JH_ERR_ARG: return "invalid argument";
+    default: return "unknown status";
+    }
+}
+
+const char* jules_hip_last_error(void) { return g_last_error.c_str(); }
+
+int jules_hip_gemm_bias_act(int dtype, int act, const void* A, const void* B, const float* bias,
+                            void* C, int M, int N, int K, void* stream) {
+    if (!valid_act(act)) return fail(JH_ERR_ACT, "gemm: activation code %d", act);
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "gemm: M=%d N=%d K=%d", M, N, K);
+    if ((int64_t)M * K > kMaxElems || (int64_t)K * N > kMaxElems || (int64_t)M * N > kMaxElems)
+        return fail(JH_ERR_SHAPE, "gemm: M=%d N=%d K=%d too large", M, N, K);
+    if (dtype != JH_F32 && dtype != JH_BF16) return fail(JH_ERR_DTYPE, "gemm: dtype %d", dtype);
+    if (M == 0 || N == 0) return JH_OK;
+    if (!C || (K > 0 && (!A || !B))) return fail(JH_ERR_NULL, "gemm: null A, B or C");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == JH_F32) {
+        if (!aligned(A, 4) || !aligned(B, 4) || !aligned(C, 4) || !aligned(bias, 4))
+            return fail(JH_ERR_ALIGN, "gemm f32: operands must be 4-byte aligned");
+        return check_hip(jh::launch_gemm_f32(act, static_cast<const float*>(A),
+                                             static_cast<const float*>(B), bias,
+                                             static_cast<float*>(C), M, N, K, s),
+                         "gemm f32 launch");
+    }
+    if (M % 8 || N % 8 || K % 8)
+        return fail(JH_ERR_UNSUPPORTED, "gemm bf16: M, N, K must be multiples of 8 (got %d %d %d)",
+                    M, N, K);
+    if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 2) || !aligned(bias, 4))
+        return fail(JH_ERR_ALIGN, "gemm bf16: A and B must be 16-byte aligned");
+    return check_hip(jh::launch_gemm_bf16(act, static_cast<const uint16_t*>(A),
+                                          static_cast<const uint16_t*>(B), bias,
+                                          static_cast<uint16_t*>(C), M, N, K, s),
+                     "gemm bf16 launch");
+}
+
+int jules_hip_activation(int act, float* out, const float* in, int64_t n, void* stream) {
+    if (!valid_act(act)) return fail(JH_ERR_ACT, "activation: code %d", act);
+    if (n < 0 || n > kMaxElems) return fail(JH_ERR_SHAPE, "activation: n=%lld", (long long)n);
+    if (n == 0) return JH_OK;
+    if (!out || !in) return fail(JH_ERR_NULL, "activation: null pointer");
+    if (!aligned(out, 4) || !aligned(in, 4)) return fail(JH_ERR_ALIGN, "activation: alignment");
+    return check_hip(jh::launch_activation(act, out, in, n, static_cast<hipStream_t>(stream)),
+                     "activation launch");
+}
+
+int jules_hip_flash_attn_fwd(int dtype, int causal, float scale, const void* Q, const void* K,
+                             const void* V, void* O, float* lse, int B, int H, int S, int D,
+                             void* stream) {
+    if (dtype != JH_F32 && dtype != JH_BF16) return fail(JH_ERR_DTYPE, "flash: dtype %d", dtype);
+    if (B < 0 || H < 0 || S < 0) return fail(JH_ERR_SHAPE, "flash: B=%d H=%d S=%d", B, H, S);
+    if (D != 64 && D != 128) return fail(JH_ERR_UNSUPPORTED, "flash: head_dim %d (64 or 128)", D);
+    if (!(std::isfinite(scale) && scale > 0.0f)) return fail(JH_ERR_ARG, "flash: scale %g", scale);
+    if (causal != 0 && causal != 1) return fail(JH_ERR_ARG, "flash: causal must be 0 or 1");
+    if ((int64_t)B * H * S * D > kMaxElems) return fail(JH_ERR_SHAPE, "flash: too large");
+    if (B == 0 || H == 0 || S == 0) return JH_OK;
+    if (!Q || !K || !V || !O) return fail(JH_ERR_NULL, "flash: null Q, K, V or O");
+    if (!aligned(Q, 16) || !aligned(K, 16) || !aligned(V, 16) || !aligned(O, 16) ||
+        !aligned(lse, 4))
+        return fail(JH_ERR_ALIGN, "flash: Q, K, V, O must be 16-byte aligned");
+    return check_hip(jh::launch_flash_fwd(dtype, causal, scale, Q, K, V, O, lse, B, H, S, D,
+                                          static_cast<hipStream_t>(stream)),
+                     "flash launch");
+}
+
+size_t jules_hip_w8a16_workspace_size(int M, int N, int K) {
+    if (M < 1 || M > 16 || N < 16 || N % 16 || K < 2 || K % 2) return 0;
+    return jh::w8a16_workspace_size(M, N, K);
+}
+
+int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W, const float* scale,
+                                  const float* bias, void* y, int M, int N, int K,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    if (!valid_act(act)) return fail(JH_ERR_ACT, "w8a16: activation code %d", act);
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "w8a16: M=%d N=%d K=%d", M, N, K);
+    if (M == 0 || N == 0) return JH_OK;
+    if (M > 16 || N % 16 || K % 2 || K == 0)
+        return fail(JH_ERR_UNSUPPORTED, "w8a16: needs 1<=M<=16, N%%16==0, K even >0 (got %d %d %d)",
+                    M, N, K);
+    if ((int64_t)K * N > kMaxElems) return fail(JH_ERR_SHAPE, "w8a16: too large");
+    if (!x || !W || !scale || !y) return fail(JH_ERR_NULL, "w8a16: null x, W, scale or y");
+    if (!aligned(W, 16) || !aligned(x, 4) || !aligned(y, 4) || !aligned(scale, 4) ||
+        !aligned(bias, 4))
+        return fail(JH_ERR_ALIGN, "w8a16: W must be 16-byte aligned, x/y/scale/bias 4-byte");
+    const size_t need = jh::w8a16_workspace_size(M, N, K);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(JH_ERR_WORKSPACE, "w8a16: workspace %zu bytes, need %zu", workspace_bytes, need);
+    if (!aligned(workspace, 16)) return fail(JH_ERR_ALIGN, "w8a16: workspace alignment");
+    return check_hip(jh::launch_w8a16(act, static_cast<const uint16_t*>(x), W, scale, bias,
+                                      static_cast<uint16_t*>(y), M, N, K, workspace,
+                                      static_cast<hipStream_t>(stream)),
+                     "w8a16 launch");
+}
+
+int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
+                          float scale_A, float scale_B, const float* bias, void* stream) {
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "matmulInt8: M=%d N=%d K=%d", M, N, K);
+    if (K > 131072) return fail(JH_ERR_SHAPE, "matmulInt8: K=%d exceeds exact int32 range", K);
+    if ((int64_t)M * K > kMaxElems || (int64_t)K * N > kMaxElems || (int64_t)M * N > kMaxElems)
+        return fail(JH_ERR_SHAPE, "matmulInt8: too large");
+    if (M == 0 || N == 0) return JH_OK;
+    if (!C || (K > 0 && (!A || !B))) return fail(JH_ERR_NULL, "matmulInt8: null A, B or C");
+    if (!aligned(C, 4) || !aligned(bias, 4)) return fail(JH_ERR_ALIGN, "matmulInt8: alignment");
+    return check_hip(jh::launch_matmul_int8(A, B, C, M, N, K, scale_A, scale_B, bias,
+                                            static_cast<hipStream_t>(stream)),
+                     "matmulInt8 launch");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Registry: extern_kernel / custom_call names -> descriptor entry points.
+// ---------------------------------------------------------------------------
+namespace {
+
+const void* addr(const jh_tensor& t) {
+    int esz = t.dtype == JH_F32 || t.dtype == JH_I32 ? 4 : t.dtype == JH_BF16 ? 2 : 1;
+    return static_cast<const char*>(t.data) + t.offset * esz;
+}
+void* addr_mut(jh_tensor& t) { return const_cast<void*>(addr(t)); }
+
+bool contiguous(const jh_tensor& t) {
+    if (t.rank < 0 || t.rank > 6) return false;
+    int64_t s = 1;
+    for (int i = t.rank - 1; i >= 0; --i) {
+        if (t.sizes[i] < 0) return false;
+        if (t.sizes[i] != 1 && t.strides[i] != s) return false;
+        s *= t.sizes[i];
+    }
+    return true;
+}
+
+int64_t numel(const jh_tensor& t) {
+    int64_t n = 1;
+    for (int i = 0; i < t.rank; ++i) n *= t.sizes[i];
+    return n;
+}
+
+// parse "key=value" out of a comma separated backend_config
+bool config_float(const char* cfg, const char* key, float* out) {
+    if (!cfg) return false;
+    const size_t kl = strlen(key);
+    const char* p = cfg;
+    while (*p) {
+        while (*p == ' ' || *p == ',') ++p;
+        if (strncmp(p, key, kl) == 0 && p[kl] == '=') {
+            char* end = nullptr;
+            const float v = strtof(p + kl + 1, &end);
+            if (end == p + kl + 1) return false;
+            *out = v;
+            return true;
+        }
+        while (*p && *p != ',') ++p;
+    }
+    return false;
+}
+
+int matmul_desc(int act, bool with_bias, int n_in, const jh_tensor* in, int n_out,
+                jh_tensor* out, void* stream) {
+    if (n_in != (with_bias ? 3 : 2) || n_out != 1 || !in || !out)
+        return fail(JH_ERR_ARG, "matmul: expected %d inputs and 1 output", with_bias ? 3 : 2);
+    const jh_tensor &a = in[0], &b = in[1];
+    jh_tensor& c = out[0];
+    if (a.rank != 2 || b.rank != 2 || c.rank != 2) return fail(JH_ERR_SHAPE, "matmul: rank != 2");
+    if (!contiguous(a) || !contiguous(b) || !contiguous(c))
+        return fail(JH_ERR_UNSUPPORTED, "matmul: non-contiguous operand");
+    const int64_t M = a.sizes[0], K = a.sizes[1], N = b.sizes[1];
+    if (b.sizes[0] != K || c.sizes[0] != M || c.sizes[1] != N)
+        return fail(JH_ERR_SHAPE, "matmul: shape mismatch");
+    if (a.dtype != b.dtype || a.dtype != c.dtype) return fail(JH_ERR_DTYPE, "matmul: dtype mismatch");
+    const float* bias = nullptr;
+    if (with_bias) {
+        if (in[2].dtype != JH_F32 || numel(in[2]) != N || !contiguous(in[2]))
+            return fail(JH_ERR_SHAPE, "matmul: bias must be fp32 [N]");
+        bias = static_cast<const float*>(addr(in[2]));
+    }
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return fail(JH_ERR_SHAPE, "matmul: dims");
+    return jules_hip_gemm_bias_act(a.dtype, act, addr(a), addr(b), bias, addr_mut(c), (int)M,
+                                   (int)N, (int)K, stream);
+}
+
+#define MATMUL_ENTRY(fname, ACT, BIAS)                                                      \
+    int fname(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) { \
+        return matmul_desc(ACT, BIAS, ni, in, no, out, s);                                  \
+    }
+MATMUL_ENTRY(k_matmul, JH_ACT_NONE, false)
+MATMUL_ENTRY(k_matmul_relu, JH_ACT_RELU, false)
+MATMUL_ENTRY(k_matmul_sigmoid, JH_ACT_SIGMOID, false)
+MATMUL_ENTRY(k_matmul_tanh, JH_ACT_TANH, false)
+MATMUL_ENTRY(k_matmul_gelu, JH_ACT_GELU, false)
+MATMUL_ENTRY(k_matmul_bias, JH_ACT_NONE, true)
+MATMUL_ENTRY(k_matmul_bias_relu, JH_ACT_RELU, true)
+MATMUL_ENTRY(k_matmul_bias_sigmoid, JH_ACT_SIGMOID, true)
+MATMUL_ENTRY(k_matmul_bias_tanh, JH_ACT_TANH, true)
+MATMUL_ENTRY(k_matmul_bias_gelu, JH_ACT_GELU, true)
+MATMUL_ENTRY(k_matmul_bias_silu, JH_ACT_SILU, true)
+
+int k_gelu(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
+    if (ni != 1 || no != 1 || !in || !out) return fail(JH_ERR_ARG, "fusedGelu: 1 in, 1 out");
+    if (in[0].dtype != JH_F32 || out[0].dtype != JH_F32)
+        return fail(JH_ERR_DTYPE, "fusedGelu: fp32 only");
+    if (!contiguous(in[0]) || !contiguous(out[0]) || numel(in[0]) != numel(out[0]))
+        return fail(JH_ERR_SHAPE, "fusedGelu: shape");
+    return jules_hip_activation(JH_ACT_GELU, static_cast<float*>(addr_mut(out[0])),
+                                static_cast<const float*>(addr(in[0])), numel(in[0]), s);
+}
+
+int attention_desc(int causal, int ni, const jh_tensor* in, int no, jh_tensor* out,
+                   const char* cfg, void* s) {
+    if (ni != 3 || no != 1 || !in || !out) return fail(JH_ERR_ARG, "attention: 3 in, 1 out");
+    for (int i = 0; i < 3; ++i)
+        if (in[i].rank != 4 || !contiguous(in[i])) return fail(JH_ERR_SHAPE, "attention: [B,H,S,D]");
+    if (out[0].rank != 4 || !contiguous(out[0])) return fail(JH_ERR_SHAPE, "attention: out");
+    for (int d = 0; d < 4; ++d)
+        if (in[1].sizes[d] != in[0].sizes[d] || in[2].sizes[d] != in[0].sizes[d] ||
+            out[0].sizes[d] != in[0].sizes[d])
+            return fail(JH_ERR_SHAPE, "attention: Q, K, V, O shapes differ");
+    const int dt = in[0].dtype;
+    if (in[1].dtype != dt || in[2].dtype != dt || out[0].dtype != dt)
+        return fail(JH_ERR_DTYPE, "attention: dtype mismatch");
+    const int D = (int)in[0].sizes[3];
+    float scale = 1.0f / sqrtf((float)D);  // reference FlashAttention.h:135
+    config_float(cfg, "scale", &scale);
+    return jules_hip_flash_attn_fwd(dt, causal, scale, addr(in[0]), addr(in[1]), addr(in[2]),
+                                    addr_mut(out[0]), nullptr, (int)in[0].sizes[0],
+                                    (int)in[0].sizes[1], (int)in[0].sizes[2], D, s);
+}
+int k_attn(int ni, const jh_tensor* in, int no, jh_tensor* out, const char* c, void* s) {
+    return attention_desc(0, ni, in, no, out, c, s);
+}
+int k_attn_causal(int ni, const jh_tensor* in, int no, jh_tensor* out, const char* c, void* s) {
+    return attention_desc(1, ni, in, no, out, c, s);
+}
+
+// One zero-filled W8A16 workspace per device, grown on demand, for callers of
+// the registry who cannot pass one.  Guarded by a mutex; calls that share a
+// device through this path are serialised by the caller's stream order.
+std::mutex g_ws_mu;
+void* g_ws[64];
+size_t g_ws_bytes[64];
+
+int registry_workspace(size_t need, void** ws) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return fail(JH_ERR_HIP, "w8a16 registry: hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (g_ws_bytes[dev] < need) {
+        if (g_ws[dev]) (void)hipFree(g_ws[dev]);
+        g_ws[dev] = nullptr;
+        g_ws_bytes[dev] = 0;
+        void* p = nullptr;
+        if (hipMalloc(&p, need) != hipSuccess) return fail(JH_ERR_HIP, "w8a16 registry: hipMalloc");
+        if (hipMemset(p, 0, need) != hipSuccess) return fail(JH_ERR_HIP, "w8a16 registry: hipMemset");
+        g_ws[dev] = p;
+        g_ws_bytes[dev] = need;
+    }
+    *ws = g_ws[dev];
+    return JH_OK;
+}
+
+int k_w8a16_silu(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
+    if ((ni != 3 && ni != 4) || no != 1 || !in || !out)
+        return fail(JH_ERR_ARG, "matmulW8A16BiasSilu: (x, W, scale[, bias]) -> y");
+    const jh_tensor &x = in[0], &w = in[1], &sc = in[2];
+    jh_tensor& y = out[0];
+    if (x.rank != 2 || w.rank != 2 || y.rank != 2 || !contiguous(x) || !contiguous(w) ||
+        !contiguous(y) || !contiguous(sc))
+        return fail(JH_ERR_SHAPE, "matmulW8A16BiasSilu: 2-D contiguous operands");
+    if (x.dtype != JH_BF16 || w.dtype != JH_I8 || sc.dtype != JH_F32 || y.dtype != JH_BF16)
+        return fail(JH_ERR_DTYPE, "matmulW8A16BiasSilu: x bf16, W int8, scale fp32, y bf16");
+    const int64_t M = x.sizes[0], K = x.sizes[1], N = w.sizes[1];
+    if (w.sizes[0] != K || y.sizes[0] != M || y.sizes[1] != N || numel(sc) != N)
+        return fail(JH_ERR_SHAPE, "matmulW8A16BiasSilu: shape mismatch");
+    const float* bias = nullptr;
+    if (ni == 4) {
+        if (in[3].dtype != JH_F32 || numel(in[3]) != N || !contiguous(in[3]))
+            return fail(JH_ERR_SHAPE, "matmulW8A16BiasSilu: bias fp32 [N]");
+        bias = static_cast<const float*>(addr(in[3]));
+    }
+    const size_t need = jules_hip_w8a16_workspace_size((int)M, (int)N, (int)K);
+    void* ws = nullptr;
+    if (need) {
+        const int st = registry_workspace(need, &ws);
+        if (st != JH_OK) return st;
+    }
+    return jules_hip_w8a16_gemm_bias_act(JH_ACT_SILU, addr(x), static_cast<const int8_t*>(addr(w)),
+                                         static_cast<const float*>(addr(sc)), bias, addr_mut(y),
+                                         (int)M, (int)N, (int)K, ws, need, s);
+}
+
+int k_int8(int ni, const jh_tensor* in, int no, jh_tensor* out, const char* cfg, void* s) {
+    if ((ni != 2 && ni != 3) || no != 1 || !in || !out)
+        return fail(JH_ERR_ARG, "matmulInt8: (A, B[, bias]) -> C");
+    const jh_tensor &a = in[0], &b = in[1];
+    jh_tensor& c = out[0];
+    if (a.rank != 2 || b.rank != 2 || c.rank != 2 || !contiguous(a) || !contiguous(b) ||
+        !contiguous(c))
+        return fail(JH_ERR_SHAPE, "matmulInt8: 2-D contiguous operands");
+    if (a.dtype != JH_I8 || b.dtype != JH_I8 || c.dtype != JH_F32)
+        return fail(JH_ERR_DTYPE, "matmulInt8: int8 x int8 -> fp32");
+    const int64_t M = a.sizes[0], K = a.sizes[1], N = b.sizes[1];
+    if (b.sizes[0] != K || c.sizes[0] != M || c.sizes[1] != N)
+        return fail(JH_ERR_SHAPE, "matmulInt8: shape mismatch");
+    float sa = 1.0f, sb = 1.0f;
+    config_float(cfg, "scale_a", &sa);
+    config_float(cfg, "scale_b", &sb);
+    const float* bias = nullptr;
+    if (ni == 3) {
+        if (in[2].dtype != JH_F32 || numel(in[2]) != N || !contiguous(in[2]))
+            return fail(JH_ERR_SHAPE, "matmulInt8: bias fp32 [N]");
+        bias = static_cast<const float*>(addr(in[2]));
+    }
+    return jules_hip_matmul_int8(static_cast<const int8_t*>(addr(a)),
+                                 static_cast<const int8_t*>(addr(b)),
+                                 static_cast<float*>(addr_mut(c)), (int)M, (int)N, (int)K, sa, sb,
+                                 bias, s);
+}
+
+struct Entry {
+    const char* name;
+    jh_kernel_fn fn;
+};
+
+// Names emitted by KernelRoutingPass (lib/Passes/KernelRoutingPass.cpp:144-166,
+// :189-211, :287, :409) and listed in KernelRoutingPass.h:13-23, then the
+// names this library adds.
+const Entry kRegistry[] = {
+    {"fusedMatmulRelu", k_matmul_relu},
+    {"fusedMatmulSigmoid", k_matmul_sigmoid},
+    {"fusedMatmulTanh", k_matmul_tanh},
+    {"fusedMatmulGelu", k_matmul_gelu},
+    {"fusedMatmulBiasRelu", k_matmul_bias_relu},
+    {"fusedMatmulBiasSigmoid", k_matmul_bias_sigmoid},
+    {"fusedMatmulBiasTanh", k_matmul_bias_tanh},
+    {"fusedGelu", k_gelu},
+    {"matmulInt8", k_int8},
+    {"flashAttention", k_attn},
+    {"fusedMatmul", k_matmul},
+    {"fusedMatmulBias", k_matmul_bias},
+    {"fusedMatmulBiasGelu", k_matmul_bias_gelu},
+    {"fusedMatmulBiasSilu", k_matmul_bias_silu},
+    {"flashAttentionCausal", k_attn_causal},
+    {"matmulW8A16BiasSilu", k_w8a16_silu},
+};
+constexpr int kRegistrySize = sizeof(kRegistry) / sizeof(kRegistry[0]);
+
+}  // namespace
+
+extern "C" {
+
+jh_kernel_fn jules_hip_lookup(const char* name) {
+    if (!name) {
+        fail(JH_ERR_NULL, "lookup: null name");
+        return nullptr;
+    }
+    for (int i = 0; i < kRegistrySize; ++i)
+        if (strcmp(kRegistry[i].name, name) == 0) return kRegistry[i].fn;
+    fail(JH_ERR_NOT_FOUND, "lookup: no kernel named '%s'", name);
+    return nullptr;
+}
+
+int jules_hip_kernel_count(void) { return kRegistrySize; }
+
+const char* jules_hip_kernel_name(int index) {
+    if (index < 0 || index >= kRegistrySize) return nullptr;
+    return kRegistry[index].name;
+}
+
+}  // extern "C"

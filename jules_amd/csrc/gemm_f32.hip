@@ -1,0 +1,134 @@
+// gemm_f32.hip - fp32 fused GEMM + bias + activation for gfx950.
+//
+// Semantics follow the reference's tiled AVX-512 kernel
+// (include/jules/Kernel/FusedKernels.h:378-458, bias epilogue :308-313):
+// every output is ONE sequential fma chain over k = 0..K-1 starting from 0
+// (the reference reloads the stored partial sum per K tile and keeps chaining,
+// :401-406), followed by + bias[j] and the vector-path activation.  Each thread
+// owns a TM x TN block of outputs and walks k in order, so the GPU reproduces
+// those bits exactly; that rules out split-K and MFMA (whose internal
+// accumulation order differs) for this dtype.  Parallelism comes from output
+// tiles only.
+//
+// Data path: A and B tiles are staged through LDS (A transposed to k-major so
+// a thread reads its TM rows as one vector), one barrier pair per BK slice.
+// The K tail is handled by a uniform trip count, never by zero padding (an
+// extra fma(0, b, acc) could turn a -0 partial sum into +0).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace jh {
+namespace {
+
+template <int BM, int BN, int BK, int TM, int TN, int ACT>
+__global__ __launch_bounds__((BM / TM) * (BN / TN)) void gemm_f32_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ bias,
+    float* __restrict__ C, int M, int N, int K) {
+    constexpr int TX = BN / TN;          // threads along N
+    constexpr int NT = (BM / TM) * TX;   // threads per block
+    __shared__ float As[BK][BM + 4];     // k-major copy of the A tile
+    __shared__ float Bs[BK][BN + 4];
+
+    const int tid = threadIdx.x;
+    const int tx = tid % TX, ty = tid / TX;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    float acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
+
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        const int kc = min(BK, K - k0);
+        for (int e = tid; e < BM * BK; e += NT) {
+            const int m = e / BK, k = e % BK;
+            float v = 0.0f;
+            if (m0 + m < M && k < kc) v = A[(int64_t)(m0 + m) * K + k0 + k];
+            As[k][m] = v;
+        }
+        for (int e = tid; e < BK * BN; e += NT) {
+            const int k = e / BN, n = e % BN;
+            float v = 0.0f;
+            if (k < kc && n0 + n < N) v = B[(int64_t)(k0 + k) * N + n0 + n];
+            Bs[k][n] = v;
+        }
+        __syncthreads();
+        for (int k = 0; k < kc; ++k) {
+            float a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) a[i] = As[k][ty * TM + i];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = Bs[k][tx * TN + j];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int m = m0 + ty * TM + i;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = n0 + tx * TN + j;
+            if (n >= N) continue;
+            float v = acc[i][j];
+            if (bias) v = v + bias[n];
+            C[(int64_t)m * N + n] = activate<ACT>(v);
+        }
+    }
+}
+
+template <int BM, int BN, int BK, int TM, int TN, int ACT>
+hipError_t run(const float* A, const float* B, const float* bias, float* C, int M, int N, int K,
+               hipStream_t s) {
+    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+    dim3 block((BM / TM) * (BN / TN));
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, TM, TN, ACT>), grid, block, 0, s, A, B, bias,
+                       C, M, N, K);
+    return hipGetLastError();
+}
+
+template <int ACT>
+__global__ void activation_kernel(float* out, const float* __restrict__ in, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = activate<ACT>(in[i]);
+}
+
+}  // namespace
+
+hipError_t launch_gemm_f32(int act, const float* A, const float* B, const float* bias, float* C,
+                           int M, int N, int K, hipStream_t s) {
+    // 64x64 tiles (4x4 per thread) once there are enough of them to cover the
+    // 256 CUs twice over; 32x32 tiles (2x2 per thread) for small problems such
+    // as 512^3, which then still launches 256 workgroups.
+    const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
+    hipError_t e = hipSuccess;
+    if (tiles64 >= 512) {
+        JH_DISPATCH_ACT(act, ACT, e = (run<64, 64, 16, 4, 4, ACT>(A, B, bias, C, M, N, K, s)));
+    } else {
+        JH_DISPATCH_ACT(act, ACT, e = (run<32, 32, 16, 2, 2, ACT>(A, B, bias, C, M, N, K, s)));
+    }
+    return e;
+}
+
+hipError_t launch_activation(int act, float* out, const float* in, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const int threads = 256;
+    int64_t blocks = (n + threads - 1) / threads;
+    if (blocks > 4096) blocks = 4096;
+    hipError_t e = hipSuccess;
+    JH_DISPATCH_ACT(act, ACT, {
+        hipLaunchKernelGGL(activation_kernel<ACT>, dim3((unsigned)blocks), dim3(threads), 0, s,
+                           out, in, n);
+        e = hipGetLastError();
+    });
+    return e;
+}
+
+}  // namespace jh

@@ -1,0 +1,229 @@
+// kernel_shims.cpp - jules::kernel C++ entry points (include/jules_hip_kernel.hpp)
+// implemented on the C ABI.  Host buffers are staged through device memory
+// and the call is synchronous, as the reference's CPU kernels are.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "jules_hip.h"
+#include "jules_hip_kernel.hpp"
+
+namespace jules {
+namespace kernel {
+namespace {
+
+thread_local int g_status = JH_OK;
+thread_local std::string g_error;
+
+void record(int st) {
+    g_status = st;
+    g_error = st == JH_OK ? std::string() : std::string(jules_hip_last_error());
+}
+
+bool is_device_ptr(const void* p) {
+    if (!p) return false;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice;
+}
+
+// A device view of a caller buffer: the buffer itself when it already lives
+// on the device, otherwise a device copy (copied in if `in`, back if `out`).
+class DevBuf {
+public:
+    DevBuf(const void* host, size_t bytes, bool in, bool out)
+        : host_(const_cast<void*>(host)), bytes_(bytes), out_(out) {
+        if (!host || bytes == 0) return;
+        if (is_device_ptr(host)) {
+            dev_ = host_;
+            return;
+        }
+        if (hipMalloc(&dev_, bytes) != hipSuccess) {
+            dev_ = nullptr;
+            ok_ = false;
+            return;
+        }
+        owned_ = true;
+        if (in && hipMemcpy(dev_, host, bytes, hipMemcpyHostToDevice) != hipSuccess) ok_ = false;
+    }
+    ~DevBuf() {
+        if (owned_) (void)hipFree(dev_);
+    }
+    bool finish() {  // copy results back; false on failure
+        if (!ok_) return false;
+        if (owned_ && out_ && hipMemcpy(host_, dev_, bytes_, hipMemcpyDeviceToHost) != hipSuccess)
+            return false;
+        return true;
+    }
+    bool ok() const { return ok_; }
+    void* get() const { return dev_; }
+
+private:
+    void* host_;
+    void* dev_ = nullptr;
+    size_t bytes_;
+    bool out_;
+    bool owned_ = false;
+    bool ok_ = true;
+};
+
+void run_gemm(const float* A, const float* B, const float* bias, float* C, int M, int N, int K,
+              int act) {
+    if (M < 0 || N < 0 || K < 0) return record(JH_ERR_SHAPE);
+    DevBuf a(A, sizeof(float) * (size_t)M * K, true, false);
+    DevBuf b(B, sizeof(float) * (size_t)K * N, true, false);
+    DevBuf bi(bias, bias ? sizeof(float) * (size_t)N : 0, true, false);
+    DevBuf c(C, sizeof(float) * (size_t)M * N, false, true);
+    if (!a.ok() || !b.ok() || !bi.ok() || !c.ok()) return record(JH_ERR_HIP);
+    int st = jules_hip_gemm_bias_act(JH_F32, act, a.get(), b.get(),
+                                     static_cast<const float*>(bi.get()), c.get(), M, N, K, nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !c.finish()) st = JH_ERR_HIP;
+    record(st);
+}
+
+void run_attention(float* out, const float* Q, const float* K, const float* V, int B, int H,
+                   int S, int D) {
+    if (B < 0 || H < 0 || S < 0 || D <= 0) return record(JH_ERR_SHAPE);
+    const size_t bytes = sizeof(float) * (size_t)B * H * S * D;
+    DevBuf q(Q, bytes, true, false), k(K, bytes, true, false), v(V, bytes, true, false);
+    DevBuf o(out, bytes, false, true);
+    if (!q.ok() || !k.ok() || !v.ok() || !o.ok()) return record(JH_ERR_HIP);
+    const float scale = 1.0f / sqrtf((float)D);  // reference FlashAttention.h:135
+    int st = jules_hip_flash_attn_fwd(JH_F32, 0, scale, q.get(), k.get(), v.get(), o.get(),
+                                      nullptr, B, H, S, D, nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !o.finish()) st = JH_ERR_HIP;
+    record(st);
+}
+
+}  // namespace
+
+int lastStatus() { return g_status; }
+const char* lastError() { return g_error.c_str(); }
+
+size_t TileConfig::footprintBytes(int, int, int) const {
+    return ((size_t)tile_m * tile_k + (size_t)tile_k * tile_n + (size_t)tile_m * tile_n) * 4;
+}
+bool TileConfig::fitsInCache(size_t cacheBytes, int M, int N, int K) const {
+    return footprintBytes(M, N, K) <= cacheBytes;
+}
+
+CacheInfo CacheInfo::detect() {
+    CacheInfo c{160 * 1024, 4 * 1024 * 1024, 256UL * 1024 * 1024, 128, 256};
+    int dev = 0;
+    hipDeviceProp_t p;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) {
+        if (p.maxSharedMemoryPerMultiProcessor > 0) c.l1d_bytes = p.maxSharedMemoryPerMultiProcessor;
+        if (p.l2CacheSize > 0) c.l2_bytes = (size_t)p.l2CacheSize;
+        if (p.multiProcessorCount > 0) c.num_cores = p.multiProcessorCount;
+    } else {
+        (void)hipGetLastError();
+    }
+    return c;
+}
+
+TilePlanner::TilePlanner(const CacheInfo& cache) : cache_(cache) {}
+
+// The gfx950 tile table used by libjules_hip: fp32 SIMT tiles 64x64x16
+// (32x32x16 when fewer than 512 such tiles exist); bf16 MFMA tiles 256x256x64.
+TileConfig TilePlanner::computeAnalytical(int M, int N, int) const {
+    const long tiles64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    if (tiles64 >= 512) return TileConfig{64, 64, 16};
+    return TileConfig{32, 32, 16};
+}
+TileConfig TilePlanner::getTileConfig(int M, int N, int K) { return computeAnalytical(M, N, K); }
+
+ExecutionArena::ExecutionArena(size_t maxSize) : maxSize_(maxSize) {
+    void* p = nullptr;
+    if (hipMalloc(&p, maxSize_) != hipSuccess || hipMemset(p, 0, maxSize_) != hipSuccess) {
+        (void)hipGetLastError();
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        maxSize_ = 0;
+    }
+    buffer_ = static_cast<char*>(p);
+}
+ExecutionArena::~ExecutionArena() {
+    if (buffer_) (void)hipFree(buffer_);
+}
+void* ExecutionArena::allocateBytes(size_t bytes) {
+    const size_t aligned_offset = (offset_ + 255) & ~size_t(255);
+    if (!buffer_ || aligned_offset + bytes > maxSize_) {
+        record(JH_ERR_WORKSPACE);
+        return nullptr;
+    }
+    offset_ = aligned_offset + bytes;
+    if (offset_ > highWaterMark_) highWaterMark_ = offset_;
+    return buffer_ + aligned_offset;
+}
+void ExecutionArena::resetAndZero() {
+    if (buffer_ && offset_) (void)hipMemset(buffer_, 0, offset_);
+    offset_ = 0;
+}
+
+void fusedMatmulRelu(const float* X, const float* W, float* output, int M, int K, int N) {
+    run_gemm(X, W, nullptr, output, M, N, K, JH_ACT_RELU);
+}
+
+void fusedMatmulBiasRelu(const float* X, const float* W, const float* bias, float* output, int M,
+                         int K, int N) {
+    run_gemm(X, W, bias, output, M, N, K, JH_ACT_RELU);
+}
+
+void tiledMatmulWithActivation(const float* A, const float* B, float* C, int M, int N, int K,
+                               const TileConfig&, ActivationType act) {
+    run_gemm(A, B, nullptr, C, M, N, K, static_cast<int>(act));
+}
+
+void fusedGelu(float* output, const float* input, int N) {
+    if (N < 0) return record(JH_ERR_SHAPE);
+    const size_t bytes = sizeof(float) * (size_t)N;
+    DevBuf in(input, bytes, true, false), out(output, bytes, false, true);
+    if (!in.ok() || !out.ok()) return record(JH_ERR_HIP);
+    int st = jules_hip_activation(JH_ACT_GELU, static_cast<float*>(out.get()),
+                                  static_cast<const float*>(in.get()), N, nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !out.finish()) st = JH_ERR_HIP;
+    record(st);
+}
+
+void matmulInt8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K, float scale_A,
+                float scale_B, const float* bias, ExecutionArena*) {
+    if (M < 0 || N < 0 || K < 0) return record(JH_ERR_SHAPE);
+    DevBuf a(A, (size_t)M * K, true, false), b(B, (size_t)K * N, true, false);
+    DevBuf bi(bias, bias ? sizeof(float) * (size_t)N : 0, true, false);
+    DevBuf c(C, sizeof(float) * (size_t)M * N, false, true);
+    if (!a.ok() || !b.ok() || !bi.ok() || !c.ok()) return record(JH_ERR_HIP);
+    int st = jules_hip_matmul_int8(static_cast<const int8_t*>(a.get()),
+                                   static_cast<const int8_t*>(b.get()),
+                                   static_cast<float*>(c.get()), M, N, K, scale_A, scale_B,
+                                   static_cast<const float*>(bi.get()), nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !c.finish()) st = JH_ERR_HIP;
+    record(st);
+}
+
+void flashAttention(float* output, const float* Q, const float* K, const float* V, int batch,
+                    int heads, int seq, int head_dim, ExecutionArena&, TilePlanner&) {
+    run_attention(output, Q, K, V, batch, heads, seq, head_dim);
+}
+
+void attention(float* output, const float* Q, const float* K, const float* V, int batch, int heads,
+               int seq, int head_dim, ExecutionArena&, TilePlanner&) {
+    run_attention(output, Q, K, V, batch, heads, seq, head_dim);
+}
+
+void standardAttention(float* output, const float* Q, const float* K, const float* V, int batch,
+                       int heads, int seq, int head_dim, ExecutionArena& arena) {
+    run_attention(output, Q, K, V, batch, heads, seq, head_dim);
+    arena.reset();  // reference FlashAttention.h:99
+}
+
+}  // namespace kernel
+}  // namespace jules

@@ -1,0 +1,26 @@
+// launch.hpp - internal launchers of libjules_hip (not part of the C ABI).
+// Arguments have been validated by capi.cpp before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace jh {
+
+hipError_t launch_gemm_f32(int act, const float* A, const float* B, const float* bias,
+                           float* C, int M, int N, int K, hipStream_t s);
+hipError_t launch_gemm_bf16(int act, const uint16_t* A, const uint16_t* B, const float* bias,
+                            uint16_t* C, int M, int N, int K, hipStream_t s);
+hipError_t launch_activation(int act, float* out, const float* in, int64_t n, hipStream_t s);
+hipError_t launch_flash_fwd(int dtype, int causal, float scale, const void* Q, const void* K,
+                            const void* V, void* O, float* lse, int B, int H, int S, int D,
+                            hipStream_t s);
+size_t w8a16_workspace_size(int M, int N, int K);
+hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float* scale,
+                        const float* bias, uint16_t* y, int M, int N, int K, void* ws,
+                        hipStream_t s);
+hipError_t launch_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
+                              float scale_a, float scale_b, const float* bias, hipStream_t s);
+
+}  // namespace jh

@@ -1,0 +1,142 @@
+"""torch-tensor front end of the C ABI.
+
+Each function validates device, dtype and contiguity, then calls the
+corresponding jules_hip_* entry point on torch's current HIP stream.  torch
+provides device memory and the stream only; all arithmetic happens in
+libjules_hip.so.  Names follow the reference's jules::kernel functions
+(include/jules/Kernel/FusedKernels.h, FlashAttention.h).
+"""
+import numpy as np
+
+import torch
+
+from . import _lib
+from ._lib import ACT, BF16, F32, check, lib
+
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _need(t, name, dtypes, device=None):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name}: dtype {t.dtype} not in {dtypes}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def _act(act):
+    return ACT[act] if isinstance(act, str) else int(act)
+
+
+def gemm_bias_act(A, B, bias=None, act="none", out=None):
+    """C = act(A @ B + bias).  fp32 (bit-exact with the reference's fma chain) or
+    bf16 (MFMA, fp32 accumulate).  Mirrors tiledMatmulWithActivation /
+    fusedMatmulBiasRelu (FusedKernels.h:378, :265)."""
+    _need(A, "A", (torch.float32, torch.bfloat16))
+    _need(B, "B", (A.dtype,), A.device)
+    M, K = A.shape
+    K2, N = B.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    if bias is not None:
+        _need(bias, "bias", (torch.float32,), A.device)
+        if bias.numel() != N:
+            raise ValueError("bias must have N elements")
+    if out is None:
+        out = torch.empty((M, N), dtype=A.dtype, device=A.device)
+    else:
+        _need(out, "out", (A.dtype,), A.device)
+    check(lib().jules_hip_gemm_bias_act(_DT[A.dtype], _act(act), _ptr(A), _ptr(B), _ptr(bias),
+                                        _ptr(out), M, N, K, _stream(A)))
+    return out
+
+
+def activation(x, act="gelu", out=None):
+    """out = act(x), fp32; act='gelu' is fusedGelu (FusedKernels.h:606)."""
+    _need(x, "x", (torch.float32,))
+    if out is None:
+        out = torch.empty_like(x)
+    else:
+        _need(out, "out", (torch.float32,), x.device)
+    check(lib().jules_hip_activation(_act(act), _ptr(out), _ptr(x), x.numel(), _stream(x)))
+    return out
+
+
+def default_scale(D):
+    """1.0f / sqrtf((float)D) evaluated in fp32, as FlashAttention.h:135 does."""
+    return float(np.float32(1.0) / np.sqrt(np.float32(D)))
+
+
+def flash_attention(Q, K, V, causal=False, scale=None, out=None, lse=None):
+    """Flash-attention forward, [B,H,S,D]; scale defaults to 1/sqrtf(D) as in
+    flashAttention (FlashAttention.h:135)."""
+    _need(Q, "Q", (torch.float32, torch.bfloat16))
+    _need(K, "K", (Q.dtype,), Q.device)
+    _need(V, "V", (Q.dtype,), Q.device)
+    if Q.dim() != 4 or K.shape != Q.shape or V.shape != Q.shape:
+        raise ValueError("Q, K, V must share a [B,H,S,D] shape")
+    B, H, S, D = Q.shape
+    if scale is None:
+        scale = default_scale(D)
+    if out is None:
+        out = torch.empty_like(Q)
+    else:
+        _need(out, "out", (Q.dtype,), Q.device)
+    if lse is not None:
+        _need(lse, "lse", (torch.float32,), Q.device)
+    check(lib().jules_hip_flash_attn_fwd(_DT[Q.dtype], int(bool(causal)), float(scale), _ptr(Q),
+                                         _ptr(K), _ptr(V), _ptr(out), _ptr(lse), B, H, S, D,
+                                         _stream(Q)))
+    return out
+
+
+def w8a16_workspace(M, N, K, device):
+    n = lib().jules_hip_w8a16_workspace_size(M, N, K)
+    return torch.zeros(max(n, 16), dtype=torch.uint8, device=device)
+
+
+def w8a16_gemm(x, W, scale, bias=None, act="silu", out=None, workspace=None):
+    """y = act(scale * (x @ W) + bias); x bf16 [M,K], W int8 [K,N]."""
+    _need(x, "x", (torch.bfloat16,))
+    _need(W, "W", (torch.int8,), x.device)
+    _need(scale, "scale", (torch.float32,), x.device)
+    M, K = x.shape
+    K2, N = W.shape
+    if K != K2:
+        raise ValueError("inner dimensions differ")
+    if bias is not None:
+        _need(bias, "bias", (torch.float32,), x.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if workspace is None:
+        workspace = w8a16_workspace(M, N, K, x.device)
+    check(lib().jules_hip_w8a16_gemm_bias_act(_act(act), _ptr(x), _ptr(W), _ptr(scale),
+                                              _ptr(bias), _ptr(out), M, N, K, _ptr(workspace),
+                                              workspace.numel(), _stream(x)))
+    return out
+
+
+def matmul_int8(A, B, scale_a, scale_b, bias=None, out=None):
+    """matmulInt8 (FusedKernels.h:867) with the scalar path's semantics."""
+    _need(A, "A", (torch.int8,))
+    _need(B, "B", (torch.int8,), A.device)
+    M, K = A.shape
+    _, N = B.shape
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=A.device)
+    if bias is not None:
+        _need(bias, "bias", (torch.float32,), A.device)
+    check(lib().jules_hip_matmul_int8(_ptr(A), _ptr(B), _ptr(out), M, N, K, float(scale_a),
+                                      float(scale_b), _ptr(bias), _stream(A)))
+    return out

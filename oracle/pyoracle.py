@@ -1,0 +1,251 @@
+"""ctypes wrapper around oracle/liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
+never by the product package.  Every function takes and returns numpy arrays;
+bf16 tensors are passed widened to float32 (exact).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+ACT = {"none": 0, "relu": 1, "sigmoid": 2, "tanh": 3, "gelu": 4, "silu": 5}
+
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_c_int = ctypes.c_int
+_c_i64 = ctypes.c_int64
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run oracle/build_oracle.py")
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "jo_fast_exp": (ctypes.c_float, [ctypes.c_float]),
+            "jo_gelu": (ctypes.c_float, [ctypes.c_float]),
+            "jo_sigmoid": (ctypes.c_float, [ctypes.c_float]),
+            "jo_fast_tanh": (ctypes.c_float, [ctypes.c_float]),
+            "jo_silu": (ctypes.c_float, [ctypes.c_float]),
+            "jo_act": (ctypes.c_float, [_c_int, ctypes.c_float]),
+            "jo_act_array": (None, [_c_int, _f32p, _f32p, _c_i64]),
+            "jo_fast_exp_array": (None, [_f32p, _f32p, _c_i64]),
+            "jo_fused_gelu": (None, [_f32p, _f32p, _c_int]),
+            "jo_tiled_matmul_act": (None, [_f32p, _f32p, _f32p] + [_c_int] * 7),
+            "jo_matmul_bias_act": (None, [_f32p, _f32p, _f32p, _f32p] + [_c_int] * 7),
+            "jo_tile_analytical": (None, [_c_int] * 3 + [_c_i64, _c_i64, _c_int,
+                                                          ctypes.POINTER(_c_int),
+                                                          ctypes.POINTER(_c_int),
+                                                          ctypes.POINTER(_c_int)]),
+            "jo_flash_attention": (None, [_f32p] * 4 + [_c_int] * 7 + [ctypes.c_float]),
+            "jo_flash_tiles": (None, [_c_int, _c_int, _c_i64, ctypes.POINTER(_c_int),
+                                      ctypes.POINTER(_c_int)]),
+            "jo_matmul_int8": (None, [_i8p, _i8p, _f32p, _c_int, _c_int, _c_int,
+                                      ctypes.c_float, ctypes.c_float, _f32p]),
+            "jo_w8a16": (None, [_f32p, _i8p, _f32p, _f32p, _f32p] + [_c_int] * 4),
+            "jo64_act": (ctypes.c_double, [_c_int, ctypes.c_double]),
+            "jo64_gemm_bias_act": (None, [_f32p, _f32p, _f32p, _f64p] + [_c_int] * 4
+                                   + [_i32p, _c_int]),
+            "jo64_attention_head": (None, [_f32p, _f32p, _f32p, _f64p, _c_int, _c_int,
+                                           _c_int, ctypes.c_double, _i32p, _c_int]),
+            "jo64_w8a16": (None, [_f32p, _i8p, _f32p, _f32p, _f64p] + [_c_int] * 4),
+            "jo_max_threads": (_c_int, []),
+            "jo_set_threads": (None, [_c_int]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a, ctype):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def act_code(act):
+    return ACT[act] if isinstance(act, str) else int(act)
+
+
+# ---- scalar / elementwise -------------------------------------------------
+def fast_exp(x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().jo_fast_exp_array(_p(out, ctypes.c_float), _p(x, ctypes.c_float), x.size)
+    return out
+
+
+def act_array(act, x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().jo_act_array(act_code(act), _p(out, ctypes.c_float), _p(x, ctypes.c_float), x.size)
+    return out
+
+
+def fused_gelu(x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().jo_fused_gelu(_p(out, ctypes.c_float), _p(x, ctypes.c_float), x.size)
+    return out
+
+
+# ---- GEMM ----------------------------------------------------------------
+def tile_analytical(M, N, K, l1d=48 * 1024, l2=32 * 1024, avx512=True):
+    """TilePlanner::computeAnalytical.  The l2 default reproduces the
+    reference's reading of sysfs cache/index1 (the L1 instruction cache on
+    x86) as "L2" (reference ExecutionArena.h:74-76)."""
+    tm, tn, tk = _c_int(), _c_int(), _c_int()
+    lib().jo_tile_analytical(M, N, K, l1d, l2, int(avx512), ctypes.byref(tm),
+                             ctypes.byref(tn), ctypes.byref(tk))
+    return tm.value, tn.value, tk.value
+
+
+def matmul_bias_act(A, B, bias, act, tiles=None):
+    """act(A.B + bias) via the restated tiled AVX-512 kernel (fp32)."""
+    A = _f32(A)
+    B = _f32(B)
+    M, K = A.shape
+    K2, N = B.shape
+    assert K == K2
+    bias = None if bias is None else _f32(bias)
+    tm, tn, tk = tiles if tiles is not None else tile_analytical(M, N, K)
+    out = np.empty((M, N), np.float32)
+    lib().jo_matmul_bias_act(_p(A, ctypes.c_float), _p(B, ctypes.c_float),
+                             _p(bias, ctypes.c_float), _p(out, ctypes.c_float),
+                             M, K, N, tm, tn, tk, act_code(act))
+    return out
+
+
+def tiled_matmul_act(A, B, act, tiles=None):
+    A = _f32(A)
+    B = _f32(B)
+    M, K = A.shape
+    _, N = B.shape
+    tm, tn, tk = tiles if tiles is not None else tile_analytical(M, N, K)
+    out = np.empty((M, N), np.float32)
+    lib().jo_tiled_matmul_act(_p(A, ctypes.c_float), _p(B, ctypes.c_float),
+                              _p(out, ctypes.c_float), M, N, K, tm, tn, tk, act_code(act))
+    return out
+
+
+def gemm64(A, B, bias, act, rows=None):
+    A = _f32(A)
+    B = _f32(B)
+    M, K = A.shape
+    _, N = B.shape
+    bias = None if bias is None else _f32(bias)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    R = M if r is None else len(r)
+    out = np.empty((R, N), np.float64)
+    lib().jo64_gemm_bias_act(_p(A, ctypes.c_float), _p(B, ctypes.c_float),
+                             _p(bias, ctypes.c_float), _p(out, ctypes.c_double),
+                             M, N, K, act_code(act), _p(r, ctypes.c_int32), R)
+    return out
+
+
+# ---- attention -------------------------------------------------------------
+def flash_tiles(S, D, l2=32 * 1024):
+    tq, tk = _c_int(), _c_int()
+    lib().jo_flash_tiles(S, D, l2, ctypes.byref(tq), ctypes.byref(tk))
+    return tq.value, tk.value
+
+
+def flash_attention(Q, K, V, causal, scale=None, tiles=(32, 64)):
+    Q = _f32(Q)
+    K = _f32(K)
+    V = _f32(V)
+    B, H, S, D = Q.shape
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    out = np.empty_like(Q)
+    lib().jo_flash_attention(_p(out, ctypes.c_float), _p(Q, ctypes.c_float),
+                             _p(K, ctypes.c_float), _p(V, ctypes.c_float),
+                             B, H, S, D, tiles[0], tiles[1], int(causal), scale)
+    return out
+
+
+def attention64_head(q, k, v, causal, scale, rows=None):
+    """fp64 softmax attention for one head; q,k,v [S,D]."""
+    q = _f32(q)
+    k = _f32(k)
+    v = _f32(v)
+    S, D = q.shape
+    r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    R = S if r is None else len(r)
+    out = np.empty((R, D), np.float64)
+    lib().jo64_attention_head(_p(q, ctypes.c_float), _p(k, ctypes.c_float),
+                              _p(v, ctypes.c_float), _p(out, ctypes.c_double),
+                              S, D, int(causal), float(scale), _p(r, ctypes.c_int32), R)
+    return out
+
+
+def attention64(Q, K, V, causal, scale):
+    B, H, S, D = Q.shape
+    out = np.empty((B, H, S, D), np.float64)
+    for b in range(B):
+        for h in range(H):
+            out[b, h] = attention64_head(Q[b, h], K[b, h], V[b, h], causal, scale)
+    return out
+
+
+# ---- int8 ------------------------------------------------------------------
+def matmul_int8(A, B, scale_a, scale_b, bias=None):
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    M, K = A.shape
+    _, N = B.shape
+    bias = None if bias is None else _f32(bias)
+    out = np.empty((M, N), np.float32)
+    lib().jo_matmul_int8(_p(A, ctypes.c_int8), _p(B, ctypes.c_int8), _p(out, ctypes.c_float),
+                         M, N, K, float(scale_a), float(scale_b), _p(bias, ctypes.c_float))
+    return out
+
+
+def w8a16(x, W, scale, bias, act):
+    x = _f32(x)
+    W = np.ascontiguousarray(W, np.int8)
+    scale = _f32(scale)
+    bias = None if bias is None else _f32(bias)
+    M, K = x.shape
+    _, N = W.shape
+    out = np.empty((M, N), np.float32)
+    lib().jo_w8a16(_p(x, ctypes.c_float), _p(W, ctypes.c_int8), _p(scale, ctypes.c_float),
+                   _p(bias, ctypes.c_float), _p(out, ctypes.c_float), M, N, K, act_code(act))
+    return out
+
+
+def w8a16_64(x, W, scale, bias, act):
+    x = _f32(x)
+    W = np.ascontiguousarray(W, np.int8)
+    scale = _f32(scale)
+    bias = None if bias is None else _f32(bias)
+    M, K = x.shape
+    _, N = W.shape
+    out = np.empty((M, N), np.float64)
+    lib().jo64_w8a16(_p(x, ctypes.c_float), _p(W, ctypes.c_int8), _p(scale, ctypes.c_float),
+                     _p(bias, ctypes.c_float), _p(out, ctypes.c_double), M, N, K, act_code(act))
+    return out
+
+
+def max_threads():
+    return lib().jo_max_threads()
+
+
+def set_threads(n):
+    lib().jo_set_threads(int(n))

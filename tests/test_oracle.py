@@ -1,0 +1,325 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU's checker.
+
+The reference ships no golden vectors and cannot be compiled here (its kernel
+headers include <cblas.h>, absent from the image), so every function is pinned
+by what the mathematics fixes: fp64 evaluations of the textbook definitions,
+closed forms (B = I, K = 1, A = 0, one-hot activations), invariants (V = 1,
+Q = 0, causal row 0, permutation and tiling invariance) and exact brute force
+(rational arithmetic) on tiny shapes.  Each check is chosen so that a
+plausible slip in the restatement (dropped term, wrong coefficient, transposed
+operand, wrong mask) fails it.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import inputs as I
+from oracle import pyoracle as po
+
+ACTS = ["none", "relu", "sigmoid", "tanh", "gelu", "silu"]
+
+
+# ---- exact fp32 arithmetic for brute force ---------------------------------
+def _round_f32(x: Fraction) -> np.float32:
+    """Correctly rounded (ties to even) Fraction -> float32."""
+    f = np.float32(float(x))
+    best = None
+    for c in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        if not np.isfinite(c):
+            continue
+        d = abs(Fraction(float(c)) - x)
+        if best is None or d < best[0] or (d == best[0] and (int(c.view(np.uint32)) & 1) == 0):
+            best = (d, c)
+    return best[1]
+
+
+def fma32(a, b, c):
+    return _round_f32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def add32(a, b):
+    return _round_f32(Fraction(float(a)) + Fraction(float(b)))
+
+
+# ---- activations -----------------------------------------------------------
+def _sweep():
+    top = np.float32(88.0).view(np.uint32)
+    pos = np.arange(0, top, 613, dtype=np.uint32).view(np.float32)
+    return np.concatenate([pos, -pos])
+
+
+def test_fast_exp_against_fp64():
+    """Reference fast_exp_zmm (FusedKernels.h:90-133): degree-6 polynomial.
+    Measured bound 1.74e-5 relative over [-87, 88]; a dropped Horner term or a
+    wrong coefficient moves it past 1e-4, a wrong exponent bias past 0.5."""
+    x = _sweep()
+    y = po.fast_exp(x).astype(np.float64)
+    e = np.exp(x.astype(np.float64))
+    m = x > -87.0
+    rel = np.abs(y[m] - e[m]) / e[m]
+    assert rel.max() < 2.0e-5
+    assert rel.max() > 1.0e-6  # it is a polynomial, not a libm call
+    # exact points: 2^0 * p(0) = 1; clamp at -88 gives 2^-127 -> exponent bits 0 -> 0.0
+    assert po.fast_exp(np.float32([0.0]))[0] == 1.0
+    assert po.fast_exp(np.float32([-88.0, -1000.0]))[0] == 0.0
+    assert po.fast_exp(np.float32([-1000.0]))[0] == 0.0
+    assert po.fast_exp(np.float32([1000.0]))[0] == po.fast_exp(np.float32([88.0]))[0]
+
+
+def test_fast_exp_planted_mistake_is_caught():
+    """The bound above is tight enough to see the smallest plausible slip: the
+    same polynomial with its last coefficient dropped, evaluated in numpy."""
+    x = _sweep()
+    x = x[(x > -80) & (x < 80)]
+    r = (x * np.float32(1.4426950408889634)).astype(np.float32)
+    ri = np.floor(r)
+    rf = (r - ri).astype(np.float64)
+    c = [1.0, 0.693147180, 0.240226507, 0.055495506, 0.009614425, 0.001333356]  # c6 dropped
+    p = sum(ci * rf ** i for i, ci in enumerate(c))
+    y = np.ldexp(p, ri.astype(np.int64))
+    rel = np.abs(y - np.exp(x.astype(np.float64))) / np.exp(x.astype(np.float64))
+    assert rel.max() > 2.0e-5
+
+
+@pytest.mark.parametrize("act", ["sigmoid", "tanh", "gelu", "silu"])
+def test_activation_against_fp64(act):
+    x = np.linspace(-12, 12, 200001, dtype=np.float32)
+    y = po.act_array(act, x).astype(np.float64)
+    o = np.array([po.lib().jo64_act(po.ACT[act], float(v)) for v in x[::97]])
+    yo = y[::97]
+    # pointwise: |y - o| <= 1e-5 * max(|o|, |x| * 1e-3, 1e-3); normwise well under 1e-5
+    assert np.max(np.abs(yo - o)) / np.max(np.abs(o)) < 1e-5
+    # GELU(x) at large |x|: x for x >> 0, 0 for x << 0
+    if act == "gelu":
+        g = po.act_array("gelu", np.float32([-20.0, 20.0]))
+        assert g[1] == np.float32(20.0) and abs(g[0]) < 1e-6
+
+
+def test_activation_closed_forms():
+    x = np.float32([0.0, 1.0, -1.0, 3.0])
+    assert list(po.act_array("relu", np.float32([-1.0, -0.0, 2.0, np.nan]))) == [0.0, 0.0, 2.0, 0.0]
+    assert np.signbit(po.act_array("relu", np.float32([-0.0]))[0]) == np.False_  # maxps(-0, +0) = +0
+    assert po.act_array("sigmoid", np.float32([0.0]))[0] == 0.5
+    assert po.act_array("tanh", np.float32([0.0]))[0] == 0.0
+    assert po.act_array("gelu", np.float32([0.0]))[0] == 0.0
+    assert po.act_array("silu", np.float32([0.0]))[0] == 0.0
+    np.testing.assert_array_equal(po.act_array("none", x), x)
+    # gelu = 0.5 x (1 + tanh(u)) reproduced from the restated tanh and IEEE float32 ops
+    xs = np.float32([0.5, -0.75, 2.25])
+    for v in xs:
+        inner = np.float32(0.7978845608) * (v + np.float32(0.044715) * (v * (v * v)))
+        t = po.act_array("tanh", np.float32([inner]))[0]
+        assert po.act_array("gelu", np.float32([v]))[0] == np.float32(0.5) * (v * (np.float32(1.0) + t))
+
+
+def test_fused_gelu_matches_vector_path_and_tail():
+    x = I.uniform(1, 0, (37,), -4, 4)
+    y = po.fused_gelu(x)
+    np.testing.assert_array_equal(y[:32], po.act_array("gelu", x[:32]))
+    # the last 5 elements take the tanhf tail (FusedKernels.h:614-617)
+    t = x[32:].astype(np.float32)
+    tail = np.float32(0.5) * t * (np.float32(1.0) + np.tanh(
+        np.float32(0.7978845608) * (t + np.float32(0.044715) * t * t * t)))
+    np.testing.assert_allclose(y[32:], tail, rtol=2e-6, atol=1e-7)
+
+
+# ---- GEMM ----------------------------------------------------------------
+@pytest.mark.parametrize("act", ACTS)
+def test_gemm_against_fp64(act):
+    A, B, bias = I.gemm_inputs(96, 80, 130, "f32", seed=3)
+    y = po.matmul_bias_act(A, B, bias, act)
+    o = po.gemm64(A, B, bias, act)
+    assert I.rel_err(y, o) < 1e-5
+    # the fp64 oracle agrees with an independent numpy evaluation
+    z = A.astype(np.float64) @ B.astype(np.float64) + bias
+    ref = np.array([[po.lib().jo64_act(po.ACT[act], float(v)) for v in row] for row in z[:4]])
+    np.testing.assert_allclose(o[:4], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_identity_is_exact():
+    """B = I: every fma adds an exact zero except one a*1, so C = act(A + bias)
+    bit for bit; a transposed operand or dropped bias fails."""
+    A = I.uniform(5, 0, (48, 64), -3, 3)
+    bias = I.uniform(5, 2, (64,), -1, 1)
+    for act in ACTS:
+        y = po.matmul_bias_act(A, np.eye(64, dtype=np.float32), bias, act)
+        np.testing.assert_array_equal(y, po.act_array(act, A + bias))
+
+
+def test_gemm_k1_and_zero_a():
+    A = I.uniform(6, 0, (32, 1), -2, 2)
+    B = I.uniform(6, 1, (1, 48), -2, 2)
+    bias = I.uniform(6, 2, (48,), -1, 1)
+    y = po.matmul_bias_act(A, B, bias, "gelu")
+    np.testing.assert_array_equal(y, po.act_array("gelu", (A * B) + bias))
+    z = po.matmul_bias_act(np.zeros((16, 40), np.float32), I.uniform(6, 3, (40, 32), -1, 1),
+                           bias[:32], "sigmoid")
+    np.testing.assert_array_equal(z, np.broadcast_to(po.act_array("sigmoid", bias[:32] + 0.0), (16, 32)))
+
+
+def test_gemm_bruteforce_fma_chain():
+    """Exact rational fma chain on a ragged shape: every element is the
+    sequential fma over k from 0, then one rounded add of bias.  Columns past
+    the last 16-wide vector of a tile go through the scalar tail, which also
+    chains in fma."""
+    M, N, K = 3, 21, 7
+    A = I.uniform(7, 0, (M, K), -1, 1)
+    B = I.uniform(7, 1, (K, N), -1, 1)
+    bias = I.uniform(7, 2, (N,), -1, 1)
+    y = po.matmul_bias_act(A, B, bias, "none", tiles=(16, 16, 4))
+    for i in range(M):
+        for j in range(N):
+            acc = np.float32(0.0)
+            for k in range(K):
+                acc = fma32(A[i, k], B[k, j], acc)
+            assert y[i, j] == add32(acc, bias[j]), (i, j)
+
+
+def test_gemm_tile_invariance():
+    A, B, bias = I.gemm_inputs(64, 96, 200, "f32", seed=8)
+    ys = [po.matmul_bias_act(A, B, bias, "gelu", tiles=t)
+          for t in [(16, 16, 16), (32, 32, 128), (64, 96, 200), (48, 32, 24)]]
+    for y in ys[1:]:
+        np.testing.assert_array_equal(ys[0], y)
+
+
+def test_tile_planner_restatement():
+    """TilePlanner::computeAnalytical (TilePlanner.h:97-136) with this
+    container's cache sizes as the reference reads them (index0 = 48K L1d,
+    index1 = 32K L1i taken as L2): the survey's recorded picks."""
+    assert po.tile_analytical(512, 512, 512) == (32, 32, 128)
+    assert po.tile_analytical(8, 8, 8) == (16, 16, 8)
+    # K*N*4 fits 3/4 of L2 -> tile_k = K
+    assert po.tile_analytical(64, 16, 64, l2=1 << 20) == (32, 16, 64)
+    assert po.flash_tiles(1024, 64) == (4, 16)
+    assert po.flash_tiles(4096, 128) == (4, 8)
+    assert po.flash_tiles(1024, 64, l2=2 << 20) == (32, 64)
+
+
+# ---- attention ---------------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S,tiles", [(1, (32, 64)), (37, (32, 64)), (128, (4, 16)), (200, (32, 64))])
+def test_flash_against_fp64(causal, S, tiles):
+    Q, K, V = I.attn_inputs(2, 2, S, 64, "f32", seed=S)
+    scale = 1.0 / np.sqrt(64.0)
+    y = po.flash_attention(Q, K, V, causal, np.float32(scale), tiles)
+    o = po.attention64(Q, K, V, causal, float(np.float32(scale)))
+    assert I.rel_err(y, o) < 1e-5
+
+
+def test_attention64_against_numpy():
+    Q, K, V = I.attn_inputs(1, 1, 19, 64, "f32", seed=2)
+    for causal in (False, True):
+        o = po.attention64_head(Q[0, 0], K[0, 0], V[0, 0], causal, 0.125)
+        s = Q[0, 0].astype(np.float64) @ K[0, 0].astype(np.float64).T * 0.125
+        if causal:
+            s[np.triu_indices(19, 1)] = -np.inf
+        p = np.exp(s - s.max(1, keepdims=True))
+        ref = (p / p.sum(1, keepdims=True)) @ V[0, 0].astype(np.float64)
+        np.testing.assert_allclose(o, ref, rtol=1e-12, atol=1e-13)
+
+
+def test_flash_invariants():
+    B, H, S, D = 1, 2, 70, 64
+    Q, K, V = I.attn_inputs(B, H, S, D, "f32", seed=11)
+    ones = np.ones_like(V)
+    for causal in (False, True):
+        y = po.flash_attention(Q, K, ones, causal)
+        np.testing.assert_allclose(y, 1.0, rtol=0, atol=4e-7)
+        # Q = 0: uniform weights -> mean of visible V rows (prefix means if causal)
+        z = po.flash_attention(np.zeros_like(Q), K, V, causal)
+        if causal:
+            ref = np.cumsum(V.astype(np.float64), axis=2) / np.arange(1, S + 1)[None, None, :, None]
+        else:
+            ref = np.broadcast_to(V.astype(np.float64).mean(axis=2, keepdims=True), V.shape)
+        np.testing.assert_allclose(z, ref, rtol=0, atol=2e-6)
+        # causal row 0 sees only key 0: O[0] = V[0] exactly
+        if causal:
+            c = po.flash_attention(Q, K, V, True)
+            np.testing.assert_array_equal(c[:, :, 0], V[:, :, 0])
+    # non-causal: permuting keys and values together changes nothing
+    perm = np.random.default_rng(0).permutation(S)
+    a = po.flash_attention(Q, K, V, False)
+    b = po.flash_attention(Q, K[:, :, perm], V[:, :, perm], False)
+    # the weights pass through fast_exp (1.7e-5 relative), so the order of
+    # keys moves results at that level: compare at the fp32 normwise bar
+    assert I.rel_err(b, a) < 1e-5
+    # causal: changing keys/values after position i leaves rows <= i unchanged
+    K2, V2 = K.copy(), V.copy()
+    K2[:, :, 40:] += 1.0
+    V2[:, :, 40:] -= 1.0
+    c1 = po.flash_attention(Q, K, V, True)
+    c2 = po.flash_attention(Q, K2, V2, True)
+    np.testing.assert_array_equal(c1[:, :, :40], c2[:, :, :40])
+    assert not np.array_equal(c1[:, :, 40:], c2[:, :, 40:])
+
+
+def test_flash_tiling_invariance():
+    Q, K, V = I.attn_inputs(1, 1, 96, 64, "f32", seed=5)
+    ref = po.flash_attention(Q, K, V, True, tiles=(32, 64))
+    for t in [(4, 8), (4, 16), (96, 96), (16, 32)]:
+        assert I.rel_err(po.flash_attention(Q, K, V, True, tiles=t), ref) < 1e-5
+
+
+# ---- int8 / W8A16 ------------------------------------------------------------
+def test_matmul_int8_exact():
+    A = I.int8_uniform(1, 0, (9, 70))
+    B = I.int8_uniform(1, 1, (70, 33))
+    bias = I.uniform(1, 2, (33,), -1, 1)
+    sa, sb = np.float32(0.013), np.float32(0.021)
+    y = po.matmul_int8(A, B, sa, sb, bias)
+    acc = A.astype(np.int64) @ B.astype(np.int64)
+    ref = (acc.astype(np.float32) * np.float32(sa * sb)) + bias
+    np.testing.assert_array_equal(y, ref)
+    # one-hot KAT: A = e_k picks row k of B (B indexed B[k*N+j], FusedKernels.h:1053)
+    e = np.zeros((1, 70), np.int8)
+    e[0, 17] = 1
+    y1 = po.matmul_int8(e, B, 1.0, 1.0, None)
+    np.testing.assert_array_equal(y1[0], B[17].astype(np.float32))
+
+
+def test_w8a16_against_fp64_and_kat():
+    x, W, scale, bias = I.w8a16_inputs(8, 64, 256, seed=4)
+    y = po.w8a16(x, W, scale, bias, "silu")
+    o = po.w8a16_64(x, W, scale, bias, "silu")
+    assert I.rel_err(y, o) < 1e-5
+    ref = x.astype(np.float64) @ W.astype(np.float64) * scale + bias
+    ref = ref / (1 + np.exp(-ref))
+    np.testing.assert_allclose(o, ref, rtol=1e-12, atol=1e-14)
+    # one-hot x: acc = W[k0, j] exactly, y = act(W*scale + bias) bit for bit
+    xh = np.zeros((2, 256), np.float32)
+    xh[0, 5] = 1.0
+    xh[1, 200] = 1.0
+    yh = po.w8a16(xh, W, scale, bias, "silu")
+    for r, k0 in ((0, 5), (1, 200)):
+        pre = W[k0].astype(np.float32) * scale + bias
+        np.testing.assert_array_equal(yh[r], po.act_array("silu", pre))
+
+
+# ---- inputs / metric ------------------------------------------------------
+def test_inputs_deterministic_and_distributed():
+    a = I.normal(0, 1, (1 << 16,))
+    np.testing.assert_array_equal(a, I.normal(0, 1, (1 << 16,)))
+    assert not np.array_equal(a, I.normal(0, 2, (1 << 16,)))
+    assert abs(a.mean()) < 0.02 and abs(a.std() - 1) < 0.02
+    u = I.uniform(0, 0, (1 << 16,), -1, 1)
+    assert u.min() >= -1 and u.max() < 1 and abs(u.mean()) < 0.02
+    w = I.int8_uniform(0, 0, (1 << 16,))
+    assert w.min() == -127 and w.max() == 127
+    # sub-ranges are prefix independent
+    np.testing.assert_array_equal(I.bits(3, 4, 10, offset=5), I.bits(3, 4, 15)[5:])
+
+
+def test_bf16_round_matches_torch():
+    torch = pytest.importorskip("torch")
+    x = I.normal(1, 1, (100000,)) * np.float32(7.3)
+    x[:4] = [1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8, 65504.0]  # ties both ways
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(I.bf16_round(x), ref)
+
+
+def test_rel_err_metric():
+    o = np.array([1.0, -4.0, 2.0])
+    assert I.rel_err(o, o) == 0.0
+    assert I.rel_err(o + np.array([0, 0.4, 0]), o) == pytest.approx(0.1)
