@@ -31,7 +31,11 @@ def test_f32_c1_bit_exact(dev, act):
     y = _gemm_f32(dev, A, B, bias, act)
     ref = po.matmul_bias_act(A, B, bias, act)
     np.testing.assert_array_equal(y, ref)
-    assert I.rel_err(y, po.gemm64(A, B, bias, act)) < I.TOL["f32"]
+    # The reference's fast_tanh, (e^2x - 1)/(e^2x + 1) on its degree-6 fast_exp,
+    # is itself 1.26e-5 from fp64 here; bit-exact parity inherits that, so tanh
+    # alone is held to the reference's own error (1.5e-5).  C1's GELU meets 1e-5.
+    tol = 1.5e-5 if act == "tanh" else I.TOL["f32"]
+    assert I.rel_err(y, po.gemm64(A, B, bias, act)) < tol
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 16, 1), (17, 32, 5), (65, 144, 257), (128, 96, 1000),
