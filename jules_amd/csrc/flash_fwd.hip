@@ -1,9 +1,466 @@
-// flash_fwd.hip - placeholder, replaced by the MFMA flash-attention kernel.
+// flash_fwd.hip - flash-attention forward on gfx950 MFMA.
+//
+// O = softmax(scale * Q K^T [causal mask]) V per (batch, head); Q, K, V, O are
+// [B,H,S,D] row-major, D in {64, 128}.  The reference is flashAttention
+// (include/jules/Kernel/FlashAttention.h:130-309): per query tile, per key
+// tile, scores -> running row max -> rescale of the accumulator and the
+// running sum by exp(m_old - m_new) -> p = exp(s - m_new) -> acc += p V ->
+// O = acc / sum.  This kernel keeps that online-softmax recurrence and adds
+// the causal mask and an explicit scale.
+//
+// Orientation.  Scores are computed transposed, S^T = K Q^T: the MFMA's A
+// operand is a 32-key slice of K (k-dimension = head dim, contiguous in HBM),
+// its B operand 32 queries of Q.  In the 32x32 MFMA output layout every lane
+// then owns ONE query column (lane & 31) and 16 of the 32 keys, the other half
+// of the keys sitting in lane ^ 32.  Consequences:
+//   - the running max/sum are per-lane scalars; the row max needs a single
+//     exchange with lane ^ 32, the row sum none until the very end;
+//   - the accumulator rescale by exp(m_old - m_new) is a per-lane multiply;
+//   - the score registers are, after conversion, directly the B operand of
+//     O^T = V^T P^T: for key step kk the 8 keys a lane holds are
+//     {16kk + 4g + 0..3, 16kk + 8 + 4g + 0..3} (g = lane / 32), which are
+//     accumulator elements 8*(kk%2) .. 8*(kk%2)+7 of score tile kk/2.
+// V^T must supply the same 8 keys per lane: V tiles are transposed into LDS
+// (d-major, keys contiguous) with the key order inside each 16-key group
+// stored as [0-3, 8-11, 4-7, 12-15], so each operand is one 16-byte read.
+//
+// Block: 4 waves x 32 queries = 128 query rows; key tiles of 64 (bf16) or 32
+// (fp32) rows, double-buffered in LDS, loaded by the whole block.  Causal
+// blocks stop at the diagonal, waves skip key tiles that are wholly above
+// their own diagonal, and the heaviest query tiles are dispatched first.
+//
+// bf16: v_mfma_f32_32x32x16_bf16, fp32 softmax statistics, exp2 with
+// scale*log2(e) folded into one fma.  fp32: v_mfma_f32_32x32x2_f32 (full fp32
+// products), same recurrence.
 #include "common.hpp"
 #include "launch.hpp"
+
 namespace jh {
-hipError_t launch_flash_fwd(int, int, float, const void*, const void*, const void*, void*, float*,
-                            int, int, int, int, hipStream_t) {
-    return hipErrorNotSupported;
+namespace {
+
+constexpr int BQ = 128;
+constexpr int NW = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+__device__ __forceinline__ bf16x8_t pack8(const float* p) {
+    u32x4_t u;
+    u[0] = pack_bf16x2(p[0], p[1]);
+    u[1] = pack_bf16x2(p[2], p[3]);
+    u[2] = pack_bf16x2(p[4], p[5]);
+    u[3] = pack_bf16x2(p[6], p[7]);
+    return __builtin_bit_cast(bf16x8_t, u);
 }
+
+// ---------------------------------------------------------------------------
+// bf16
+// ---------------------------------------------------------------------------
+template <int D>
+struct Bf16Cfg {
+    static constexpr int BKV = 64;
+    static constexpr int KROW = D * 2;                  // bytes per K row in LDS
+    static constexpr int K_BYTES = BKV * KROW;          // K tile
+    static constexpr int V_BYTES = D * BKV * 2;         // V^T tile: D rows x BKV keys
+    static constexpr int STAGE = K_BYTES + V_BYTES;
+    static constexpr int KCH = D / 8;                   // 16-byte chunks per K row
+    static constexpr int K_CHUNKS = BKV * KCH;          // per tile
+};
+
+// K tile: row = key, 16-byte chunk c at position c ^ (row & 7)
+__device__ __forceinline__ int k_swz(int row, int chunk, int rowbytes) {
+    return row * rowbytes + ((chunk ^ (row & 7)) << 4);
+}
+// V^T tile: row = d (64 keys = 8 chunks), chunk at c ^ ((row ^ row>>3) & 7)
+__device__ __forceinline__ int v_swz(int row, int chunk) {
+    return row * 128 + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
+}
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ lse, int S,
+    float c_log2) {
+    using C = Bf16Cfg<D>;
+    constexpr int BKV = C::BKV;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 5, col = lane & 31;
+    const int bh = blockIdx.x;
+    const int nq = (S + BQ - 1) / BQ;
+    const int q0 = (nq - 1 - (int)blockIdx.y) * BQ;  // heaviest (causal) tiles first
+    const int64_t hoff = (int64_t)bh * S * D;
+    const uint16_t* Qh = Q + hoff;
+    const uint16_t* Kh = K + hoff;
+    const uint16_t* Vh = V + hoff;
+
+    // this lane's query row and its Q fragments (B operand of S^T = K Q^T)
+    const int qw0 = q0 + wave * 32;
+    const int qrow = qw0 + col;
+    bf16x8_t qf[D / 16];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+        u32x4_t v = {0u, 0u, 0u, 0u};
+        if (qrow < S) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * D + ks * 16 + 8 * g);
+        qf[ks] = __builtin_bit_cast(bf16x8_t, v);
+    }
+
+    const int kv_end = CAUSAL ? min(S, q0 + BQ) : S;
+    const int n_kv = (kv_end + BKV - 1) / BKV;
+
+    // ---- staging: K chunks t + 256 i; V as 4-key x 8-dim blocks ----
+    // V quartet u (keys 4u..4u+3 of the tile) lands in octet 2*(u/4) + (u&1),
+    // half (u>>1)&1, so every octet chunk of a V^T row holds the 8 keys one
+    // PV k-step needs in one lane group.
+    constexpr int KPT = (C::K_CHUNKS + 255) / 256;
+    u32x4_t rk[KPT], rv[4];
+    const int v_u = tid & 15;                 // key quartet
+    const int v_db = tid >> 4;                // d block: d = 8*v_db .. +7
+    const bool v_thread = v_db < D / 8;
+    const int v_oct = 2 * (v_u >> 2) + (v_u & 1);
+    const int v_half = (v_u >> 1) & 1;
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + 256 * i;
+            const int key = c / C::KCH, ch = c % C::KCH;
+            u32x4_t v = {0u, 0u, 0u, 0u};
+            if (c < C::K_CHUNKS && k0 + key < S)
+                v = *reinterpret_cast<const u32x4_t*>(Kh + (int64_t)(k0 + key) * D + ch * 8);
+            rk[i] = v;
+        }
+        if (v_thread) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int key = k0 + 4 * v_u + e;
+                u32x4_t v = {0u, 0u, 0u, 0u};
+                if (key < S) v = *reinterpret_cast<const u32x4_t*>(Vh + (int64_t)key * D + 8 * v_db);
+                rv[e] = v;
+            }
+        }
+    };
+    auto lstore = [&](int stage) {
+        uint8_t* Ks = smem + stage * C::STAGE;
+        uint8_t* Vs = Ks + C::K_BYTES;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + 256 * i;
+            if (c < C::K_CHUNKS)
+                *reinterpret_cast<u32x4_t*>(Ks + k_swz(c / C::KCH, c % C::KCH, C::KROW)) = rk[i];
+        }
+        if (v_thread) {
+            // 4 (keys) x 8 (d) transpose: LDS row d gets this quartet's 4 keys
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                u32x2_t t;
+                t[0] = __builtin_amdgcn_perm(rv[1][j >> 1], rv[0][j >> 1], sel);
+                t[1] = __builtin_amdgcn_perm(rv[3][j >> 1], rv[2][j >> 1], sel);
+                *reinterpret_cast<u32x2_t*>(Vs + v_swz(8 * v_db + j, v_oct) + 8 * v_half) = t;
+            }
+        }
+    };
+
+    f32x16_t acc_o[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[i][e] = 0.0f;
+    float m_run = kNegInf;  // running max of scaled scores, log2 domain
+    float l_run = 0.0f;     // this lane's partial running sum (its 16 keys per tile)
+
+    auto compute = [&](int stage, int k0) {
+        if (CAUSAL && k0 > qw0 + 31) return;  // whole tile above this wave's diagonal
+        const uint8_t* Ks = smem + stage * C::STAGE;
+        const uint8_t* Vs = Ks + C::K_BYTES;
+        f32x16_t s[BKV / 32];
+#pragma unroll
+        for (int mt = 0; mt < BKV / 32; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[mt][e] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+#pragma unroll
+            for (int mt = 0; mt < BKV / 32; ++mt) {
+                const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
+                    Ks + k_swz(mt * 32 + col, 2 * ks + g, C::KROW));
+                s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[mt], 0, 0, 0);
+            }
+        }
+        // masks: keys past S, and (causal) keys after this lane's query
+        const bool need_mask = (k0 + BKV > S) || (CAUSAL && k0 + BKV - 1 > qw0);
+        if (need_mask) {
+#pragma unroll
+            for (int mt = 0; mt < BKV / 32; ++mt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = k0 + mt * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+                    if (key >= S || (CAUSAL && key > qrow)) s[mt][e] = kNegInf;
+                }
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int mt = 0; mt < BKV / 32; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][e]);
+        mx = fmaxf(mx, xor32(mx));
+        const float m_new = fmaxf(m_run, mx * c_log2);
+        const float m_use = (m_new == kNegInf) ? 0.0f : m_new;  // row with no visible key yet
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        m_run = m_new;
+        float ls = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < BKV / 32; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][e], c_log2, -m_use));
+                s[mt][e] = p;
+                ls += p;
+            }
+        l_run = __builtin_fmaf(l_run, alpha, ls);
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+        // O^T += V^T P^T
+#pragma unroll
+        for (int kk = 0; kk < BKV / 16; ++kk) {
+            float pv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pv[e] = s[kk >> 1][8 * (kk & 1) + e];
+            const bf16x8_t pf = pack8(pv);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(Vs + v_swz(dt * 32 + col, 2 * kk + g));
+                acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[dt], 0, 0, 0);
+            }
+        }
+    };
+
+    if (n_kv > 0) {
+        gload(0);
+        lstore(0);
+        __syncthreads();
+        for (int j = 0; j < n_kv; ++j) {
+            const bool more = j + 1 < n_kv;
+            if (more) gload((j + 1) * BKV);
+            compute(j & 1, j * BKV);
+            if (more) lstore((j + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // ---- epilogue: O = acc / l, bf16; lse = (m + log2 l) * ln 2 ----
+    const float l_tot = l_run + xor32(l_run);
+    const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+    if (qrow < S) {
+        uint16_t* Orow = O + hoff + (int64_t)qrow * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                u32x2_t w;
+                w[0] = pack_bf16x2(acc_o[dt][4 * jb + 0] * inv, acc_o[dt][4 * jb + 1] * inv);
+                w[1] = pack_bf16x2(acc_o[dt][4 * jb + 2] * inv, acc_o[dt][4 * jb + 3] * inv);
+                *reinterpret_cast<u32x2_t*>(Orow + dt * 32 + 8 * jb + 4 * g) = w;
+            }
+        if (lse && g == 0)
+            lse[(int64_t)bh * S + qrow] = (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32: same recurrence on v_mfma_f32_32x32x2_f32.  The 32x32x2 A/B operands
+// are one fp32 per lane (row/col = lane & 31, k = lane >> 5), so K and V are
+// read from LDS as [key][d] rows without any transpose: for the PV product
+// k-step (j, i) pairs keys 8j+i (lanes 0-31) and 8j+4+i (lanes 32-63), which
+// are exactly the score accumulator element 4j+i each lane already holds.
+// ---------------------------------------------------------------------------
+template <int D>
+struct F32Cfg {
+    static constexpr int BKV = 32;
+    static constexpr int ROWF = D + 4;  // padded row (floats): rows shift by 16 B
+    static constexpr int K_FLOATS = BKV * ROWF;
+    static constexpr int STAGE_FLOATS = 2 * K_FLOATS;  // K then V
+    static constexpr int CHUNKS = BKV * D / 4;         // 16-byte chunks per tile
+};
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_fwd_f32(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ lse, int S, float c_log2) {
+    using C = F32Cfg<D>;
+    constexpr int BKV = C::BKV;
+    __shared__ __attribute__((aligned(16))) float smem[2 * C::STAGE_FLOATS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 5, col = lane & 31;
+    const int bh = blockIdx.x;
+    const int nq = (S + BQ - 1) / BQ;
+    const int q0 = (nq - 1 - (int)blockIdx.y) * BQ;
+    const int64_t hoff = (int64_t)bh * S * D;
+    const float* Qh = Q + hoff;
+    const float* Kh = K + hoff;
+    const float* Vh = V + hoff;
+    const int qw0 = q0 + wave * 32;
+    const int qrow = qw0 + col;
+
+    float qf[D / 2];  // Q[qrow][2 ks + g]
+#pragma unroll
+    for (int ks = 0; ks < D / 2; ++ks) qf[ks] = (qrow < S) ? Qh[(int64_t)qrow * D + 2 * ks + g] : 0.0f;
+
+    const int kv_end = CAUSAL ? min(S, q0 + BQ) : S;
+    const int n_kv = (kv_end + BKV - 1) / BKV;
+    constexpr int PT = (C::CHUNKS + 255) / 256;
+    f32x4_t rk[PT], rv[PT];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int c = tid + 256 * i;
+            const int key = c / (D / 4), ch = c % (D / 4);
+            f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+            if (c < C::CHUNKS && k0 + key < S) {
+                a = *reinterpret_cast<const f32x4_t*>(Kh + (int64_t)(k0 + key) * D + 4 * ch);
+                b = *reinterpret_cast<const f32x4_t*>(Vh + (int64_t)(k0 + key) * D + 4 * ch);
+            }
+            rk[i] = a;
+            rv[i] = b;
+        }
+    };
+    auto lstore = [&](int stage) {
+        float* Ks = smem + stage * C::STAGE_FLOATS;
+        float* Vs = Ks + C::K_FLOATS;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int c = tid + 256 * i;
+            if (c < C::CHUNKS) {
+                const int key = c / (D / 4), ch = c % (D / 4);
+                *reinterpret_cast<f32x4_t*>(Ks + key * C::ROWF + 4 * ch) = rk[i];
+                *reinterpret_cast<f32x4_t*>(Vs + key * C::ROWF + 4 * ch) = rv[i];
+            }
+        }
+    };
+
+    f32x16_t acc_o[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[i][e] = 0.0f;
+    float m_run = kNegInf, l_run = 0.0f;
+
+    auto compute = [&](int stage, int k0) {
+        if (CAUSAL && k0 > qw0 + 31) return;
+        const float* Ks = smem + stage * C::STAGE_FLOATS;
+        const float* Vs = Ks + C::K_FLOATS;
+        f32x16_t s;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < D / 2; ++ks)
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[col * C::ROWF + 2 * ks + g], qf[ks], s, 0, 0, 0);
+        const bool need_mask = (k0 + BKV > S) || (CAUSAL && k0 + BKV - 1 > qw0);
+        if (need_mask) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
+                if (key >= S || (CAUSAL && key > qrow)) s[e] = kNegInf;
+            }
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[e]);
+        mx = fmaxf(mx, xor32(mx));
+        const float m_new = fmaxf(m_run, mx * c_log2);
+        const float m_use = (m_new == kNegInf) ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        m_run = m_new;
+        float ls = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], c_log2, -m_use));
+            s[e] = p;
+            ls += p;
+        }
+        l_run = __builtin_fmaf(l_run, alpha, ls);
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = 8 * j + 4 * g + i;
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt)
+                    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * C::ROWF + dt * 32 + col],
+                                                                     s[4 * j + i], acc_o[dt], 0, 0, 0);
+            }
+    };
+
+    if (n_kv > 0) {
+        gload(0);
+        lstore(0);
+        __syncthreads();
+        for (int j = 0; j < n_kv; ++j) {
+            const bool more = j + 1 < n_kv;
+            if (more) gload((j + 1) * BKV);
+            compute(j & 1, j * BKV);
+            if (more) lstore((j + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    const float l_tot = l_run + xor32(l_run);
+    const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+    if (qrow < S) {
+        float* Orow = O + hoff + (int64_t)qrow * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                f32x4_t w;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = acc_o[dt][4 * jb + i] * inv;
+                *reinterpret_cast<f32x4_t*>(Orow + dt * 32 + 8 * jb + 4 * g) = w;
+            }
+        if (lse && g == 0)
+            lse[(int64_t)bh * S + qrow] = (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f;
+    }
+}
+
+template <typename KFN, typename T>
+hipError_t go(KFN kfn, const void* Q, const void* K, const void* V, void* O, float* lse, int BH,
+              int S, float c_log2, hipStream_t s) {
+    const int nq = (S + BQ - 1) / BQ;
+    hipLaunchKernelGGL(kfn, dim3(BH, nq), dim3(NW * 64), 0, s, static_cast<const T*>(Q),
+                       static_cast<const T*>(K), static_cast<const T*>(V), static_cast<T*>(O), lse,
+                       S, c_log2);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_flash_fwd(int dtype, int causal, float scale, const void* Q, const void* K,
+                            const void* V, void* O, float* lse, int B, int H, int S, int D,
+                            hipStream_t s) {
+    const int BH = B * H;
+    if (BH > 2147483647 / 1 || (S + BQ - 1) / BQ > 65535) return hipErrorInvalidValue;
+    const float c = scale * kLog2e;
+    if (dtype == JH_BF16) {
+        if (D == 128)
+            return causal ? go<decltype(&flash_fwd_bf16<128, true>), uint16_t>(&flash_fwd_bf16<128, true>, Q, K, V, O, lse, BH, S, c, s)
+                          : go<decltype(&flash_fwd_bf16<128, false>), uint16_t>(&flash_fwd_bf16<128, false>, Q, K, V, O, lse, BH, S, c, s);
+        return causal ? go<decltype(&flash_fwd_bf16<64, true>), uint16_t>(&flash_fwd_bf16<64, true>, Q, K, V, O, lse, BH, S, c, s)
+                      : go<decltype(&flash_fwd_bf16<64, false>), uint16_t>(&flash_fwd_bf16<64, false>, Q, K, V, O, lse, BH, S, c, s);
+    }
+    if (D == 128)
+        return causal ? go<decltype(&flash_fwd_f32<128, true>), float>(&flash_fwd_f32<128, true>, Q, K, V, O, lse, BH, S, c, s)
+                      : go<decltype(&flash_fwd_f32<128, false>), float>(&flash_fwd_f32<128, false>, Q, K, V, O, lse, BH, S, c, s);
+    return causal ? go<decltype(&flash_fwd_f32<64, true>), float>(&flash_fwd_f32<64, true>, Q, K, V, O, lse, BH, S, c, s)
+                  : go<decltype(&flash_fwd_f32<64, false>), float>(&flash_fwd_f32<64, false>, Q, K, V, O, lse, BH, S, c, s);
+}
+
 }  // namespace jh
