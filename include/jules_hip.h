@@ -134,7 +134,8 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale,
  * fp32 [N] or NULL, y bf16 [M,N].  fp32 accumulation; the int8 -> fp32
  * dequantisation is exact.  Deterministic: the split-K reduction sums the
  * partials in a fixed order.
- * Constraints: 1 <= M <= 16, N % 16 == 0, K % 2 == 0, W 16-byte aligned.
+ * Constraints: 1 <= M <= 16, N % 16 == 0, K % 8 == 0, W and x 16-byte
+ * aligned.
  * workspace: device memory of at least jules_hip_w8a16_workspace_size(M,N,K)
  * bytes, zero-filled before its first use; the kernel leaves it zeroed again
  * (counters are reset by the last block), so one workspace can serve any

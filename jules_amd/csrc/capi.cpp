@@ -128,7 +128,7 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale, const void* Q, 
 }
 
 size_t jules_hip_w8a16_workspace_size(int M, int N, int K) {
-    if (M < 1 || M > 16 || N < 16 || N % 16 || K < 2 || K % 2) return 0;
+    if (M < 1 || M > 16 || N < 16 || N % 16 || K < 8 || K % 8) return 0;
     return jh::w8a16_workspace_size(M, N, K);
 }
 
@@ -138,14 +138,14 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W, const
     if (!valid_act(act)) return fail(JH_ERR_ACT, "w8a16: activation code %d", act);
     if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "w8a16: M=%d N=%d K=%d", M, N, K);
     if (M == 0 || N == 0) return JH_OK;
-    if (M > 16 || N % 16 || K % 2 || K == 0)
-        return fail(JH_ERR_UNSUPPORTED, "w8a16: needs 1<=M<=16, N%%16==0, K even >0 (got %d %d %d)",
+    if (M > 16 || N % 16 || K % 8 || K == 0)
+        return fail(JH_ERR_UNSUPPORTED, "w8a16: needs 1<=M<=16, N%%16==0, K%%8==0, K>0 (got %d %d %d)",
                     M, N, K);
     if ((int64_t)K * N > kMaxElems) return fail(JH_ERR_SHAPE, "w8a16: too large");
     if (!x || !W || !scale || !y) return fail(JH_ERR_NULL, "w8a16: null x, W, scale or y");
-    if (!aligned(W, 16) || !aligned(x, 4) || !aligned(y, 4) || !aligned(scale, 4) ||
+    if (!aligned(W, 16) || !aligned(x, 16) || !aligned(y, 2) || !aligned(scale, 4) ||
         !aligned(bias, 4))
-        return fail(JH_ERR_ALIGN, "w8a16: W must be 16-byte aligned, x/y/scale/bias 4-byte");
+        return fail(JH_ERR_ALIGN, "w8a16: W and x must be 16-byte aligned, scale/bias 4-byte");
     const size_t need = jh::w8a16_workspace_size(M, N, K);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(JH_ERR_WORKSPACE, "w8a16: workspace %zu bytes, need %zu", workspace_bytes, need);

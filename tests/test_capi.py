@@ -126,6 +126,7 @@ def test_w8a16_validation():
     assert f(5, P, P, P, None, P, 17, 64, 64, P, 1 << 20, None) == UNSUP
     assert f(5, P, P, P, None, P, 8, 40, 64, P, 1 << 20, None) == UNSUP
     assert f(5, P, P, P, None, P, 8, 64, 63, P, 1 << 20, None) == UNSUP
+    assert f(5, P, P, P, None, P, 8, 64, 60, P, 1 << 20, None) == UNSUP
     assert f(5, None, P, P, None, P, 8, 64, 64, P, 1 << 20, None) == NULL
     assert f(5, P, P + 4, P, None, P, 8, 64, 64, P, 1 << 20, None) == ALIGN
     if ws > 0:

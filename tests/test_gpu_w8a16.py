@@ -1,0 +1,145 @@
+"""GPU parity of the W8A16 decode GEMM (jules_hip_w8a16_gemm_bias_act) and of
+matmulInt8 (jules_hip_matmul_int8).
+
+W8A16: within 1e-2 of the fp64 oracle; bit-exact on one-hot activations (the
+int8 index W[k*N+j] and the dequantising multiply by scale[j]).
+matmulInt8: bit-exact against the scalar path of the reference
+(FusedKernels.h:1046-1066)."""
+import numpy as np
+import pytest
+import torch
+
+from jules_amd import _lib, ops
+from oracle import inputs as I
+from oracle import pyoracle as po
+from tests.helpers import case, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+ACTS = ["none", "relu", "sigmoid", "tanh", "gelu", "silu"]
+
+
+def _w8(dev, x, W, scale, bias, act, ws=None):
+    return ops.w8a16_gemm(to_dev(x, torch.bfloat16, dev), to_dev(W, torch.int8, dev),
+                          to_dev(scale, torch.float32, dev),
+                          None if bias is None else to_dev(bias, torch.float32, dev), act,
+                          workspace=ws)
+
+
+def test_c5_full_size(dev):
+    """M=8, N=K=8192, W int8 U[-127,127], per-channel scale
+    U[1e-3,1e-2], x N(0,1) bf16, bias U[-0.1,0.1], SiLU."""
+    case("w8a16 C5 8x8192x8192 silu")
+    x, W, scale, bias = I.w8a16_inputs(8, 8192, 8192, seed=0)
+    y = to_np(_w8(dev, x, W, scale, bias, "silu"))
+    o = po.w8a16_64(x, W, scale, bias, "silu")
+    assert I.rel_err(y, o) < I.TOL["bf16"]
+    # and against the restated fp32 path
+    r = po.w8a16(x, W, scale, bias, "silu")
+    assert I.rel_err(y, r) < I.TOL["bf16"]
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 8), (3, 272, 40), (8, 512, 1000), (9, 256, 4096),
+                                   (16, 1040, 2056), (8, 8192, 64), (5, 4096, 33000)])
+def test_shapes_against_fp64(dev, M, N, K):
+    case(f"w8a16 {M}x{N}x{K}")
+    x, W, scale, bias = I.w8a16_inputs(M, N, K, seed=M + N + K)
+    y = to_np(_w8(dev, x, W, scale, bias, "silu"))
+    assert I.rel_err(y, po.w8a16_64(x, W, scale, bias, "silu")) < I.TOL["bf16"]
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_activations(dev, act):
+    case(f"w8a16 act={act}")
+    x, W, scale, bias = I.w8a16_inputs(8, 768, 1024, seed=2)
+    y = to_np(_w8(dev, x, W, scale, bias, act))
+    assert I.rel_err(y, po.w8a16_64(x, W, scale, bias, act)) < I.TOL["bf16"]
+
+
+def test_one_hot_kat_bit_exact(dev):
+    """x = one-hot rows picks W[k0, :]; then y = bf16(act(W[k0,j]*scale[j] +
+    bias[j])) exactly: pins the W[k*N+j] indexing and the one fp32 multiply
+    of the dequantisation."""
+    case("w8a16 one-hot KAT")
+    M, N, K = 8, 1024, 4096
+    _, W, scale, bias = I.w8a16_inputs(M, N, K, seed=5)
+    ks = [0, 1, 31, 32, 1000, 2047, 4090, 4095]
+    x = np.zeros((M, K), np.float32)
+    for m, k0 in enumerate(ks):
+        x[m, k0] = 1.0
+    for act in ("silu", "none", "gelu"):
+        y = _w8(dev, x, W, scale, bias, act).view(torch.int16).cpu().numpy().view(np.uint16)
+        for m, k0 in enumerate(ks):
+            pre = W[k0].astype(np.float32) * scale + bias
+            ref = I.bf16_bits(po.act_array(act, pre))
+            np.testing.assert_array_equal(y[m], ref, err_msg=f"act={act} row {m} k0={k0}")
+    # no bias: y = W*scale exactly (bf16-rounded)
+    y = _w8(dev, x, W, scale, None, "none").float().cpu().numpy()
+    for m, k0 in enumerate(ks):
+        np.testing.assert_array_equal(y[m], I.bf16_round(W[k0].astype(np.float32) * scale))
+
+
+def test_deterministic_and_workspace_reuse(dev):
+    case("w8a16 determinism, workspace reuse")
+    ws = ops.w8a16_workspace(16, 8192, 8192, dev)
+    x, W, scale, bias = I.w8a16_inputs(8, 8192, 8192, seed=7)
+    a = _w8(dev, x, W, scale, bias, "silu", ws)
+    b = _w8(dev, x, W, scale, bias, "silu", ws)
+    assert torch.equal(a, b)
+    # a different shape through the same workspace, then the first again
+    x2, W2, s2, b2 = I.w8a16_inputs(3, 512, 256, seed=8)
+    c = to_np(_w8(dev, x2, W2, s2, b2, "gelu", ws))
+    assert I.rel_err(c, po.w8a16_64(x2, W2, s2, b2, "gelu")) < I.TOL["bf16"]
+    assert torch.equal(a, _w8(dev, x, W, scale, bias, "silu", ws))
+    # the counters region is left zeroed
+    torch.cuda.synchronize()
+    assert int(ws[:256].view(torch.int32).abs().sum().item()) == 0
+
+
+def test_registry_path(dev):
+    case("w8a16 registry matmulW8A16BiasSilu")
+    x, W, scale, bias = I.w8a16_inputs(4, 512, 512, seed=9)
+    tx, tw, ts, tb = (to_dev(x, torch.bfloat16, dev), to_dev(W, torch.int8, dev),
+                      to_dev(scale, torch.float32, dev), to_dev(bias, torch.float32, dev))
+    out = torch.empty((4, 512), dtype=torch.bfloat16, device=dev)
+    ins = (_lib.JhTensor * 4)()
+    for d, t in zip(ins, (tx, tw, ts, tb)):
+        _fill(d, t)
+    o = (_lib.JhTensor * 1)()
+    _fill(o[0], out)
+    fn = _lib.lookup("matmulW8A16BiasSilu")
+    assert fn(4, ins, 1, o, None, torch.cuda.current_stream().cuda_stream) == 0
+    assert I.rel_err(to_np(out), po.w8a16_64(x, W, scale, bias, "silu")) < I.TOL["bf16"]
+
+
+# ---- matmulInt8 ---------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (8, 33, 70), (64, 64, 64), (130, 200, 515)])
+def test_int8_bit_exact(dev, M, N, K):
+    case(f"matmulInt8 {M}x{N}x{K}")
+    A = I.int8_uniform(1, 0, (M, K))
+    B = I.int8_uniform(1, 1, (K, N))
+    bias = I.uniform(1, 2, (N,), -1, 1)
+    for b in (bias, None):
+        y = ops.matmul_int8(to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev), 0.013, 0.021,
+                            None if b is None else to_dev(b, torch.float32, dev))
+        np.testing.assert_array_equal(to_np(y), po.matmul_int8(A, B, 0.013, 0.021, b))
+
+
+def test_int8_one_hot_kat(dev):
+    case("matmulInt8 one-hot KAT")
+    B = I.int8_uniform(2, 1, (70, 40))
+    A = np.zeros((3, 70), np.int8)
+    A[0, 0], A[1, 17], A[2, 69] = 1, 1, -1
+    y = to_np(ops.matmul_int8(to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev), 1.0, 1.0))
+    np.testing.assert_array_equal(y[0], B[0].astype(np.float32))
+    np.testing.assert_array_equal(y[1], B[17].astype(np.float32))
+    np.testing.assert_array_equal(y[2], -B[69].astype(np.float32))
+
+
+def _fill(d, t):
+    d.data = t.data_ptr()
+    d.offset = 0
+    d.rank = t.dim()
+    for i in range(t.dim()):
+        d.sizes[i] = t.shape[i]
+        d.strides[i] = t.stride(i)
+    d.dtype = {torch.float32: 0, torch.bfloat16: 1, torch.int8: 2}[t.dtype]
