@@ -134,13 +134,12 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale,
  * fp32 [N] or NULL, y bf16 [M,N].  fp32 accumulation; the int8 -> fp32
  * dequantisation is exact.  Deterministic: the split-K reduction sums the
  * partials in a fixed order.
- * Constraints: 1 <= M <= 16, N % 16 == 0, K % 8 == 0, W and x 16-byte
- * aligned.
+ * Constraints: 1 <= M <= 16, N % 16 == 0, K % 8 == 0; W and x 16-byte
+ * aligned, y 8-byte aligned.
  * workspace: device memory of at least jules_hip_w8a16_workspace_size(M,N,K)
- * bytes, zero-filled before its first use; the kernel leaves it zeroed again
- * (counters are reset by the last block), so one workspace can serve any
- * number of sequential calls on one stream.  Calls that overlap in time need
- * separate workspaces.
+ * bytes, 16-byte aligned (fp32 split-K partials, KS x M x N with KS <= 16);
+ * it needs no initialisation and is overwritten by every call.  Calls that
+ * overlap in time need separate workspaces.
  * No reference counterpart: the reference's int8 kernel (matmulInt8,
  * FusedKernels.h:867) is W8A8 with one scalar scale; routed name
  * "matmulW8A16BiasSilu" is new.

@@ -143,9 +143,9 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W, const
                     M, N, K);
     if ((int64_t)K * N > kMaxElems) return fail(JH_ERR_SHAPE, "w8a16: too large");
     if (!x || !W || !scale || !y) return fail(JH_ERR_NULL, "w8a16: null x, W, scale or y");
-    if (!aligned(W, 16) || !aligned(x, 16) || !aligned(y, 2) || !aligned(scale, 4) ||
+    if (!aligned(W, 16) || !aligned(x, 16) || !aligned(y, 8) || !aligned(scale, 4) ||
         !aligned(bias, 4))
-        return fail(JH_ERR_ALIGN, "w8a16: W and x must be 16-byte aligned, scale/bias 4-byte");
+        return fail(JH_ERR_ALIGN, "w8a16: W, x 16-byte, y 8-byte, scale/bias 4-byte alignment");
     const size_t need = jh::w8a16_workspace_size(M, N, K);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(JH_ERR_WORKSPACE, "w8a16: workspace %zu bytes, need %zu", workspace_bytes, need);
@@ -296,8 +296,8 @@ int k_attn_causal(int ni, const jh_tensor* in, int no, jh_tensor* out, const cha
     return attention_desc(1, ni, in, no, out, c, s);
 }
 
-// One zero-filled W8A16 workspace per device, grown on demand, for callers of
-// the registry who cannot pass one.  Guarded by a mutex; calls that share a
+// One W8A16 workspace per device, grown on demand, for callers of the
+// registry who cannot pass one.  Guarded by a mutex; calls that share a
 // device through this path are serialised by the caller's stream order.
 std::mutex g_ws_mu;
 void* g_ws[64];

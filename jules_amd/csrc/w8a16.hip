@@ -15,16 +15,19 @@
 // dot-product engine only: doing the 8 MACs per byte with v_dot2c_f32_bf16
 // would cost ~4 VALU issues per weight byte on top of the conversion and make
 // the kernel VALU-bound above the HBM time; with the MFMA the VALU work is
-// ~1.5 issues per byte.
+// ~1.5 issues per byte.  16-byte loads matter: a wave can have at most 63
+// vector loads outstanding, so narrower loads cap the bytes in flight per CU.
 //
 // Work split: a workgroup (8 waves) owns 256 columns and one of KS K-ranges;
 // every wave takes its own 32-row k-steps of that range, issuing all of its
 // weight loads for up to 4 k-steps before converting the first.  The 8 wave
-// partials are summed in LDS in a fixed tree order; the workgroup writes its
-// fp32 partial tile to the workspace; the last workgroup to finish a column
-// tile (agent-scope counter) sums the KS partials in split order, applies
-// scale, bias and the activation, and stores bf16.  The summation order is
-// fixed, so results are deterministic run to run.
+// partials are summed in LDS in a fixed tree order and the workgroup stores
+// its fp32 partial tile to the workspace.  A second, small kernel sums the KS
+// partials of every output in split order and applies scale, bias and the
+// activation.  The kernel boundary makes the partials visible; an agent-scope
+// release fence per workgroup (an L2 write-back on this part) measured
+// several microseconds.  The summation order is fixed, so results are
+// deterministic run to run.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -42,7 +45,7 @@ struct Plan {
     int steps;      // k-steps per wave
 };
 
-__host__ __device__ inline Plan plan(int K) {
+inline Plan plan(int K) {
     const int total_steps = (K + KSTEP - 1) / KSTEP;
     // aim for GROUP k-steps per wave; at most 16 splits
     int ks = (total_steps + WAVES * GROUP - 1) / (WAVES * GROUP);
@@ -53,15 +56,10 @@ __host__ __device__ inline Plan plan(int K) {
     return {ks, steps};
 }
 
-inline size_t counters_bytes(int N) { return (size_t)((N + COLS - 1) / COLS * 4 + 255) & ~size_t(255); }
-
-template <int ACT>
-__global__ __launch_bounds__(THREADS, 1) void w8a16_kernel(
-    const uint16_t* __restrict__ x, const int8_t* __restrict__ W, const float* __restrict__ scale,
-    const float* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K, int KS,
-    int steps, uint32_t* __restrict__ counters, float* __restrict__ partials) {
-    __shared__ float red[4 * 64 * 64];  // 4 wave slots x 64 lanes x 64 accumulators
-    __shared__ int last_flag;
+__global__ __launch_bounds__(THREADS, 1) void w8a16_partial_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ W, int M, int N, int K, int KS,
+    int steps, float* __restrict__ partials) {
+    __shared__ f32x4_t red[4 * 16 * 64];  // 4 wave slots x 16 accumulators x 64 lanes
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = blockIdx.x, split = blockIdx.y;
@@ -88,19 +86,24 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_kernel(
             const int st = s0 + wave + WAVES * (t0 + u);
             const bool live = (t0 + u < steps) && st < s1;
             const int kb = st * KSTEP + 8 * lg;  // this lane's 8 rows
+            // Branch-free loads: an out-of-range lane reads element 0 and the
+            // value is dropped by a select, so the compiler can wait on each
+            // load separately (vmcnt) instead of draining all of them.
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
-                u32x4_t v = {0u, 0u, 0u, 0u};
-                if (live && col_ok && kb + r < K)
-                    v = __builtin_nontemporal_load(
-                        reinterpret_cast<const u32x4_t*>(W + (int64_t)(kb + r) * N + col0));
-                wr[u][r] = v;
+                const bool ok = live && col_ok && kb + r < K;
+                const int64_t off = ok ? (int64_t)(kb + r) * N + col0 : 0;
+                const u32x4_t v =
+                    __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(W + off));
+                const u32x4_t z = {0u, 0u, 0u, 0u};
+                wr[u][r] = ok ? v : z;
             }
             // A operand: x[m = lane & 15][kb .. kb+7]
-            u32x4_t xv = {0u, 0u, 0u, 0u};
-            if (live && lc < M && kb < K)
-                xv = *reinterpret_cast<const u32x4_t*>(x + (int64_t)lc * K + kb);
-            xa[u] = __builtin_bit_cast(bf16x8_t, xv);
+            const bool xok = live && lc < M && kb < K;
+            const u32x4_t xv =
+                *reinterpret_cast<const u32x4_t*>(x + (xok ? (int64_t)lc * K + kb : 0));
+            const u32x4_t z = {0u, 0u, 0u, 0u};
+            xa[u] = __builtin_bit_cast(bf16x8_t, xok ? xv : z);
         }
 #pragma unroll
         for (int u = 0; u < GROUP; ++u) {
@@ -124,18 +127,14 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_kernel(
     }
 
     // ---- fixed-order tree reduction of the 8 wave partials in LDS ----
-    // slot layout: red[slot][e][lane] so a wave's 64 lanes write 64 consecutive floats
+    // slot layout red[slot][j][lane]: a wave's 64 lanes write 1 KiB contiguously
     auto put = [&](int slot) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) red[(slot * 64 + 4 * j + i) * 64 + lane] = acc[j][i];
+        for (int j = 0; j < 16; ++j) red[(slot * 16 + j) * 64 + lane] = acc[j];
     };
     auto add = [&](int slot) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[j][i] += red[(slot * 64 + 4 * j + i) * 64 + lane];
+        for (int j = 0; j < 16; ++j) acc[j] += red[(slot * 16 + j) * 64 + lane];
     };
     if (wave >= 4) put(wave - 4);
     __syncthreads();
@@ -147,51 +146,58 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_kernel(
     __syncthreads();
     if (wave == 1) put(0);
     __syncthreads();
-    if (wave == 0) {
-        add(0);
-        // 16x16 output layout: lane holds rows 4*lg + i, column n' = lc of
-        // MFMA j, i.e. global column col0 + j
-        float* part = partials + (int64_t)split * M * N;
+    if (wave != 0) return;
+    add(0);
+    // 16x16 output layout: lane holds rows 4*lg + i, column n' = lc of
+    // MFMA j, i.e. global column col0 + j
+    float* part = partials + (int64_t)split * M * N;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * lg + i;
-            if (m < M && col_ok) {
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * lg + i;
+        if (m < M && col_ok) {
 #pragma unroll
-                for (int j4 = 0; j4 < 4; ++j4) {
-                    f32x4_t v = {acc[4 * j4][i], acc[4 * j4 + 1][i], acc[4 * j4 + 2][i], acc[4 * j4 + 3][i]};
-                    *reinterpret_cast<f32x4_t*>(part + (int64_t)m * N + col0 + 4 * j4) = v;
-                }
+            for (int j4 = 0; j4 < 4; ++j4) {
+                f32x4_t v = {acc[4 * j4][i], acc[4 * j4 + 1][i], acc[4 * j4 + 2][i], acc[4 * j4 + 3][i]};
+                *reinterpret_cast<f32x4_t*>(part + (int64_t)m * N + col0 + 4 * j4) = v;
             }
         }
-        __threadfence();  // release the partial tile at agent scope
-        if (lane == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_ACQ_REL,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            last_flag = (prev == (uint32_t)(KS - 1));
-        }
     }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();  // acquire the other workgroups' partials
+}
 
-    // ---- last workgroup of this column tile: sum KS partials in split order ----
-    const int ncols = min(COLS, N - n0);
-    for (int e = tid; e < M * ncols; e += THREADS) {
-        const int m = e / ncols, c = n0 + e % ncols;
-        float s = 0.0f;
-        for (int p = 0; p < KS; ++p) s += __builtin_nontemporal_load(partials + ((int64_t)p * M + m) * N + c);
-        float v = s * scale[c];
-        if (bias) v = v + bias[c];
-        y[(int64_t)m * N + c] = __builtin_bit_cast(uint16_t, (__bf16)activate<ACT>(v));
+// y = act(scale * sum_p partials[p] + bias): each thread 4 consecutive
+// columns of one row, all KS partial loads issued before the first add, the
+// sum taken in split order.
+template <int ACT>
+__global__ __launch_bounds__(256) void w8a16_finalize_kernel(
+    const float* __restrict__ partials, const float* __restrict__ scale,
+    const float* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int KS) {
+    const int64_t e0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (e0 >= (int64_t)M * N) return;
+    const int m = (int)(e0 / N), c = (int)(e0 % N);
+    f32x4_t part[16];
+#pragma unroll
+    for (int p = 0; p < 16; ++p)
+        if (p < KS) part[p] = *reinterpret_cast<const f32x4_t*>(partials + ((int64_t)p * M + m) * N + c);
+    f32x4_t sum = part[0];
+#pragma unroll
+    for (int p = 1; p < 16; ++p)
+        if (p < KS) sum += part[p];
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float t = sum[i] * scale[c + i];
+        if (bias) t = t + bias[c + i];
+        v[i] = activate<ACT>(t);
     }
-    if (tid == 0) counters[tile] = 0u;  // leave the workspace ready for the next call
+    u32x2_t o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2_t*>(y + (int64_t)m * N + c) = o;
 }
 
 }  // namespace
 
 size_t w8a16_workspace_size(int M, int N, int K) {
     const Plan p = plan(K);
-    return counters_bytes(N) + (size_t)p.ks * M * N * sizeof(float);
+    return (size_t)p.ks * M * N * sizeof(float);
 }
 
 hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float* scale,
@@ -199,12 +205,16 @@ hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float
                         hipStream_t s) {
     const Plan p = plan(K);
     const int tiles = (N + COLS - 1) / COLS;
-    uint32_t* counters = static_cast<uint32_t*>(ws);
-    float* partials = reinterpret_cast<float*>(static_cast<char*>(ws) + counters_bytes(N));
-    hipError_t e = hipSuccess;
+    float* partials = static_cast<float*>(ws);
+    hipLaunchKernelGGL(w8a16_partial_kernel, dim3(tiles, p.ks), dim3(THREADS), 0, s, x, W, M, N,
+                       K, p.ks, p.steps, partials);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t quads = ((int64_t)M * N) / 4;  // N % 16 == 0
+    const unsigned blocks = (unsigned)((quads + 255) / 256);
     JH_DISPATCH_ACT(act, ACT, {
-        hipLaunchKernelGGL(w8a16_kernel<ACT>, dim3(tiles, p.ks), dim3(THREADS), 0, s, x, W,
-                           scale, bias, y, M, N, K, p.ks, p.steps, counters, partials);
+        hipLaunchKernelGGL(w8a16_finalize_kernel<ACT>, dim3(blocks), dim3(256), 0, s, partials,
+                           scale, bias, y, M, N, p.ks);
         e = hipGetLastError();
     });
     return e;

@@ -90,9 +90,9 @@ def test_deterministic_and_workspace_reuse(dev):
     c = to_np(_w8(dev, x2, W2, s2, b2, "gelu", ws))
     assert I.rel_err(c, po.w8a16_64(x2, W2, s2, b2, "gelu")) < I.TOL["bf16"]
     assert torch.equal(a, _w8(dev, x, W, scale, bias, "silu", ws))
-    # the counters region is left zeroed
-    torch.cuda.synchronize()
-    assert int(ws[:256].view(torch.int32).abs().sum().item()) == 0
+    # stale partials in the workspace do not leak into the next result
+    ws.fill_(0x7F)
+    assert torch.equal(a, _w8(dev, x, W, scale, bias, "silu", ws))
 
 
 def test_registry_path(dev):
