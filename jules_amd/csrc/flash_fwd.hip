@@ -27,7 +27,8 @@
 // Block: 4 waves x 32 queries = 128 query rows; key tiles of 64 (bf16) or 32
 // (fp32) rows, double-buffered in LDS, loaded by the whole block.  Causal
 // blocks stop at the diagonal, waves skip key tiles that are wholly above
-// their own diagonal, and the heaviest query tiles are dispatched first.
+// their own diagonal, and the heaviest query tiles of a head are dispatched
+// first; each XCD works through whole heads so K and V are re-read from L2.
 //
 // bf16: v_mfma_f32_32x32x16_bf16, fp32 softmax statistics, exp2 with
 // scale*log2(e) folded into one fma.  fp32: v_mfma_f32_32x32x2_f32 (full fp32
@@ -44,6 +45,27 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// Workgroup -> (head, query tile).  Workgroups are dealt to the 8 XCDs round
+// robin; the mapping gives each XCD whole heads (head = 8*j + xcd), all query
+// tiles of a head in a row, heaviest (causal) first.  The ~64 workgroups an
+// XCD runs at once then span about two heads, whose K and V (2 MiB each at
+// S=4096, D=128) stay in that XCD's 4 MiB L2 instead of being re-read from
+// HBM by every query tile.
+__device__ __forceinline__ void block_coords(int BH, int nq, int* bh, int* q0) {
+    const int b = blockIdx.x;
+    int head, qi;
+    if ((BH & 7) == 0) {
+        const int xcd = b & 7, i = b >> 3;
+        head = 8 * (i / nq) + xcd;
+        qi = i % nq;
+    } else {
+        head = b / nq;
+        qi = b % nq;
+    }
+    *bh = head;
+    *q0 = (nq - 1 - qi) * BQ;
+}
 
 __device__ __forceinline__ bf16x8_t pack8(const float* p) {
     u32x4_t u;
@@ -80,7 +102,7 @@ __device__ __forceinline__ int v_swz(int row, int chunk) {
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ lse, int S,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ lse, int BH, int S,
     float c_log2) {
     using C = Bf16Cfg<D>;
     constexpr int BKV = C::BKV;
@@ -88,9 +110,9 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
-    const int bh = blockIdx.x;
     const int nq = (S + BQ - 1) / BQ;
-    const int q0 = (nq - 1 - (int)blockIdx.y) * BQ;  // heaviest (causal) tiles first
+    int bh, q0;
+    block_coords(BH, nq, &bh, &q0);
     const int64_t hoff = (int64_t)bh * S * D;
     const uint16_t* Qh = Q + hoff;
     const uint16_t* Kh = K + hoff;
@@ -290,16 +312,16 @@ struct F32Cfg {
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void flash_fwd_f32(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, float* __restrict__ lse, int S, float c_log2) {
+    float* __restrict__ O, float* __restrict__ lse, int BH, int S, float c_log2) {
     using C = F32Cfg<D>;
     constexpr int BKV = C::BKV;
     __shared__ __attribute__((aligned(16))) float smem[2 * C::STAGE_FLOATS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
-    const int bh = blockIdx.x;
     const int nq = (S + BQ - 1) / BQ;
-    const int q0 = (nq - 1 - (int)blockIdx.y) * BQ;
+    int bh, q0;
+    block_coords(BH, nq, &bh, &q0);
     const int64_t hoff = (int64_t)bh * S * D;
     const float* Qh = Q + hoff;
     const float* Kh = K + hoff;
@@ -435,9 +457,9 @@ template <typename KFN, typename T>
 hipError_t go(KFN kfn, const void* Q, const void* K, const void* V, void* O, float* lse, int BH,
               int S, float c_log2, hipStream_t s) {
     const int nq = (S + BQ - 1) / BQ;
-    hipLaunchKernelGGL(kfn, dim3(BH, nq), dim3(NW * 64), 0, s, static_cast<const T*>(Q),
+    hipLaunchKernelGGL(kfn, dim3(BH * nq), dim3(NW * 64), 0, s, static_cast<const T*>(Q),
                        static_cast<const T*>(K), static_cast<const T*>(V), static_cast<T*>(O), lse,
-                       S, c_log2);
+                       BH, S, c_log2);
     return hipGetLastError();
 }
 
@@ -447,7 +469,7 @@ hipError_t launch_flash_fwd(int dtype, int causal, float scale, const void* Q, c
                             const void* V, void* O, float* lse, int B, int H, int S, int D,
                             hipStream_t s) {
     const int BH = B * H;
-    if (BH > 2147483647 / 1 || (S + BQ - 1) / BQ > 65535) return hipErrorInvalidValue;
+    if ((int64_t)BH * ((S + BQ - 1) / BQ) > 2147483647) return hipErrorInvalidValue;
     const float c = scale * kLog2e;
     if (dtype == JH_BF16) {
         if (D == 128)
