@@ -27,6 +27,17 @@ METRIC = "fused GEMM & flash-attn fwd TFLOP/s on 1 MI355X; % of MFMA/HBM rooflin
 PEAK = {"bf16": 2516.6, "f32": 157.3, "hbm": 8000.0}  # TFLOP/s, TFLOP/s, GB/s
 
 
+# HBM bytes per launch of each config's kernel(s), measured with rocprofv3
+# FETCH_SIZE and WRITE_SIZE over `bench.py --pmc` and scaled by what the same
+# counters read for a 64 MiB device copy (fetch x2.0, write x1.0).  They are
+# re-measured whenever a kernel changes; None where not measured.
+MEASURED_TRAFFIC = {
+    "c3": 202.1e6 + 34.5e6,   # gemm_bf16_kernel<GELU>
+    "c4": 809.0e6 + 268.4e6,  # flash_fwd_bf16<128, causal>
+    "c5": 68.4e6 + 2.1e6 + 2.2e6 + 0.1e6,  # w8a16 partial + finalize
+}
+
+
 def gemm_flops(M, N, K):
     return 2.0 * M * N * K
 
@@ -291,7 +302,7 @@ def main():
     dom = max(range(len(step)), key=lambda j: avg[j])
     r = step[dom]
     roofline = {"bound": r.bound, "achieved": r.rate(avg[dom]), "peak": r.peak, "unit": r.unit,
-                "frac": r.rate(avg[dom]) / r.peak, "traffic": None,
+                "frac": r.rate(avg[dom]) / r.peak, "traffic": MEASURED_TRAFFIC.get(r.name),
                 "kernel": {"c3": "gemm_bf16_kernel<GELU>", "c4": "flash_fwd_bf16"}[r.name],
                 "avg_launch_ms": avg[dom]}
     step_kernels = {x.name: {"avg_ms": a, "achieved": x.rate(a), "frac": x.rate(a) / x.peak}
