@@ -78,26 +78,44 @@ __device__ __forceinline__ bf16x8_t pack8(const float* p) {
 
 // ---------------------------------------------------------------------------
 // bf16
+//
+// K and V tiles are copied HBM -> LDS by the LDS DMA path
+// (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16 * lane),
+// with no register staging; the source address of every lane is permuted so
+// the data lands in the swizzled layout below.  Both tiles are row-major
+// [key][d] (D*2 bytes per row):
+//   K: 16-byte unit u of row r at unit u ^ (r & 7).  The S^T A operand (one
+//      key row, 8 consecutive d per lane) is one ds_read_b128; 8 consecutive
+//      rows hit distinct bank groups.
+//   V: 8-byte chunk c of row r at chunk c ^ (4 * (r & 3)).  The V^T A operand
+//      (8 keys of one d per lane) comes from two ds_read_b64_tr_b16: in each
+//      16-lane group, lane s addresses row rb + s/4, chunk cb + s%4, and lane
+//      i receives V[rb + k][4 cb + i] for k = 0..3.  The swizzle makes the 16
+//      addresses of a group fall in 16 distinct chunks.
+// Lazy rescale: the running max only moves when a tile's max exceeds it by
+// more than 8 (log2 units); p = exp2(s*c - m) then stays <= 256, exact in the
+// recurrence because the sum l uses the same m.
 // ---------------------------------------------------------------------------
 template <int D>
 struct Bf16Cfg {
     static constexpr int BKV = 64;
-    static constexpr int KROW = D * 2;                  // bytes per K row in LDS
-    static constexpr int K_BYTES = BKV * KROW;          // K tile
-    static constexpr int V_BYTES = D * BKV * 2;         // V^T tile: D rows x BKV keys
-    static constexpr int STAGE = K_BYTES + V_BYTES;
-    static constexpr int KCH = D / 8;                   // 16-byte chunks per K row
-    static constexpr int K_CHUNKS = BKV * KCH;          // per tile
+    static constexpr int ROW = D * 2;                   // bytes per K / V row in LDS
+    static constexpr int TILE = BKV * ROW;              // one operand tile
+    static constexpr int STAGE = 2 * TILE;              // K then V
+    static constexpr int UNITS = ROW / 16;              // 16-byte units per row
+    static constexpr int NSEG = TILE / 1024;            // 1 KiB DMA segments per tile
 };
 
-// K tile: row = key, 16-byte chunk c at position c ^ (row & 7)
-__device__ __forceinline__ int k_swz(int row, int chunk, int rowbytes) {
-    return row * rowbytes + ((chunk ^ (row & 7)) << 4);
+__device__ __forceinline__ int k_off(int row, int unit, int rowbytes) {
+    return row * rowbytes + ((unit ^ (row & 7)) << 4);
 }
-// V^T tile: row = d (64 keys = 8 chunks), chunk at c ^ ((row ^ row>>3) & 7)
-__device__ __forceinline__ int v_swz(int row, int chunk) {
-    return row * 128 + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
+__device__ __forceinline__ int v_off(int row, int chunk8, int rowbytes) {
+    return row * rowbytes + ((chunk8 ^ (4 * (row & 3))) << 3);
 }
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
@@ -106,7 +124,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
     float c_log2) {
     using C = Bf16Cfg<D>;
     constexpr int BKV = C::BKV;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE];
+    constexpr float kLazy = 8.0f;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
@@ -122,66 +141,32 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
     const int qw0 = q0 + wave * 32;
     const int qrow = qw0 + col;
     bf16x8_t qf[D / 16];
+    {
+        const int qr = min(qrow, S - 1);  // rows past S compute on a valid row, never stored
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-        u32x4_t v = {0u, 0u, 0u, 0u};
-        if (qrow < S) v = *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qrow * D + ks * 16 + 8 * g);
-        qf[ks] = __builtin_bit_cast(bf16x8_t, v);
+        for (int ks = 0; ks < D / 16; ++ks)
+            qf[ks] = __builtin_bit_cast(
+                bf16x8_t, *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qr * D + ks * 16 + 8 * g));
     }
 
     const int kv_end = CAUSAL ? min(S, q0 + BQ) : S;
     const int n_kv = (kv_end + BKV - 1) / BKV;
 
-    // ---- staging: K chunks t + 256 i; V as 4-key x 8-dim blocks ----
-    // V quartet u (keys 4u..4u+3 of the tile) lands in octet 2*(u/4) + (u&1),
-    // half (u>>1)&1, so every octet chunk of a V^T row holds the 8 keys one
-    // PV k-step needs in one lane group.
-    constexpr int KPT = (C::K_CHUNKS + 255) / 256;
-    u32x4_t rk[KPT], rv[4];
-    const int v_u = tid & 15;                 // key quartet
-    const int v_db = tid >> 4;                // d block: d = 8*v_db .. +7
-    const bool v_thread = v_db < D / 8;
-    const int v_oct = 2 * (v_u >> 2) + (v_u & 1);
-    const int v_half = (v_u >> 1) & 1;
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const int c = tid + 256 * i;
-            const int key = c / C::KCH, ch = c % C::KCH;
-            u32x4_t v = {0u, 0u, 0u, 0u};
-            if (c < C::K_CHUNKS && k0 + key < S)
-                v = *reinterpret_cast<const u32x4_t*>(Kh + (int64_t)(k0 + key) * D + ch * 8);
-            rk[i] = v;
-        }
-        if (v_thread) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int key = k0 + 4 * v_u + e;
-                u32x4_t v = {0u, 0u, 0u, 0u};
-                if (key < S) v = *reinterpret_cast<const u32x4_t*>(Vh + (int64_t)key * D + 8 * v_db);
-                rv[e] = v;
-            }
-        }
-    };
-    auto lstore = [&](int stage) {
+    // ---- LDS DMA of one K + V tile: wave w moves segments w, w+4, ... ----
+    constexpr int RPS = 1024 / C::ROW;  // rows per 1 KiB segment
+    auto dma = [&](int stage, int k0) {
         uint8_t* Ks = smem + stage * C::STAGE;
-        uint8_t* Vs = Ks + C::K_BYTES;
+        uint8_t* Vs = Ks + C::TILE;
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const int c = tid + 256 * i;
-            if (c < C::K_CHUNKS)
-                *reinterpret_cast<u32x4_t*>(Ks + k_swz(c / C::KCH, c % C::KCH, C::KROW)) = rk[i];
-        }
-        if (v_thread) {
-            // 4 (keys) x 8 (d) transpose: LDS row d gets this quartet's 4 keys
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                u32x2_t t;
-                t[0] = __builtin_amdgcn_perm(rv[1][j >> 1], rv[0][j >> 1], sel);
-                t[1] = __builtin_amdgcn_perm(rv[3][j >> 1], rv[2][j >> 1], sel);
-                *reinterpret_cast<u32x2_t*>(Vs + v_swz(8 * v_db + j, v_oct) + 8 * v_half) = t;
-            }
+        for (int i = 0; i < C::NSEG / NW; ++i) {
+            const int seg = i * NW + wave;
+            const int r = seg * RPS + lane / C::UNITS;  // row within the tile
+            const int up = lane % C::UNITS;             // physical 16-byte unit
+            const int64_t key = min(k0 + r, S - 1);     // rows past S read a valid row
+            const int ku = up ^ (r & 7);
+            const int vu = up ^ (2 * (r & 3));
+            __builtin_amdgcn_global_load_lds(Kh + key * D + 8 * ku, (lds_void*)(Ks + seg * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Vh + key * D + 8 * vu, (lds_void*)(Vs + seg * 1024), 16, 0, 0);
         }
     };
 
@@ -196,7 +181,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
     auto compute = [&](int stage, int k0) {
         if (CAUSAL && k0 > qw0 + 31) return;  // whole tile above this wave's diagonal
         const uint8_t* Ks = smem + stage * C::STAGE;
-        const uint8_t* Vs = Ks + C::K_BYTES;
+        const uint8_t* Vs = Ks + C::TILE;
         f32x16_t s[BKV / 32];
 #pragma unroll
         for (int mt = 0; mt < BKV / 32; ++mt)
@@ -207,7 +192,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
 #pragma unroll
             for (int mt = 0; mt < BKV / 32; ++mt) {
                 const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
-                    Ks + k_swz(mt * 32 + col, 2 * ks + g, C::KROW));
+                    Ks + k_off(mt * 32 + col, 2 * ks + g, C::ROW));
                 s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[mt], 0, 0, 0);
             }
         }
@@ -227,11 +212,20 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
         for (int mt = 0; mt < BKV / 32; ++mt)
 #pragma unroll
             for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][e]);
-        mx = fmaxf(mx, xor32(mx));
-        const float m_new = fmaxf(m_run, mx * c_log2);
-        const float m_use = (m_new == kNegInf) ? 0.0f : m_new;  // row with no visible key yet
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        m_run = m_new;
+        mx = fmaxf(mx, xor32(mx)) * c_log2;
+        // lazy rescale: move the running max only when it grows by > kLazy
+        const bool grow = mx > m_run + kLazy;
+        if (__ballot(grow)) {
+            const float m_new = grow ? mx : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+        }
+        const float m_use = (m_run == kNegInf) ? 0.0f : m_run;  // row with no visible key yet
         float ls = 0.0f;
 #pragma unroll
         for (int mt = 0; mt < BKV / 32; ++mt)
@@ -241,12 +235,9 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
                 s[mt][e] = p;
                 ls += p;
             }
-        l_run = __builtin_fmaf(l_run, alpha, ls);
-#pragma unroll
-        for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+        l_run += ls;
         // O^T += V^T P^T
+        const int vs = lane & 15, vdh = (lane >> 4) & 1;
 #pragma unroll
         for (int kk = 0; kk < BKV / 16; ++kk) {
             float pv[8];
@@ -255,21 +246,27 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
             const bf16x8_t pf = pack8(pv);
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
-                const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(Vs + v_swz(dt * 32 + col, 2 * kk + g));
+                const int c8 = 8 * dt + 4 * vdh + (vs & 3);
+                const int r0 = 16 * kk + 4 * g + (vs >> 2);
+                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(Vs + v_off(r0, c8, C::ROW)));
+                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(Vs + v_off(r0 + 8, c8, C::ROW)));
+                const s16x4_t v8[2] = {lo, hi};
+                const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, v8);
                 acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[dt], 0, 0, 0);
             }
         }
     };
 
     if (n_kv > 0) {
-        gload(0);
-        lstore(0);
+        dma(0, 0);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA writes have landed
         __syncthreads();
         for (int j = 0; j < n_kv; ++j) {
-            const bool more = j + 1 < n_kv;
-            if (more) gload((j + 1) * BKV);
+            if (j + 1 < n_kv) dma((j + 1) & 1, (j + 1) * BKV);
             compute(j & 1, j * BKV);
-            if (more) lstore((j + 1) & 1);
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
     }
