@@ -125,7 +125,14 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
     using C = Bf16Cfg<D>;
     constexpr int BKV = C::BKV;
     constexpr float kLazy = 8.0f;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+    // One array per stage and operand, and the tile loop unrolled by two, so
+    // every LDS access names its array statically: the compiler can then see
+    // that reads of one stage never alias the DMA in flight into the other
+    // and does not wait for that DMA before reading.
+    __shared__ __attribute__((aligned(1024))) uint8_t k_s0[C::TILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t v_s0[C::TILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t k_s1[C::TILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t v_s1[C::TILE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
@@ -154,9 +161,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
 
     // ---- LDS DMA of one K + V tile: wave w moves segments w, w+4, ... ----
     constexpr int RPS = 1024 / C::ROW;  // rows per 1 KiB segment
-    auto dma = [&](int stage, int k0) {
-        uint8_t* Ks = smem + stage * C::STAGE;
-        uint8_t* Vs = Ks + C::TILE;
+    auto dma = [&](uint8_t* Ks, uint8_t* Vs, int k0) {
 #pragma unroll
         for (int i = 0; i < C::NSEG / NW; ++i) {
             const int seg = i * NW + wave;
@@ -178,24 +183,26 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
     float m_run = kNegInf;  // running max of scaled scores, log2 domain
     float l_run = 0.0f;     // this lane's partial running sum (its 16 keys per tile)
 
-    auto compute = [&](int stage, int k0) {
+    auto compute = [&](const uint8_t* Ks, const uint8_t* Vs, int k0) {
         if (CAUSAL && k0 > qw0 + 31) return;  // whole tile above this wave's diagonal
-        const uint8_t* Ks = smem + stage * C::STAGE;
-        const uint8_t* Vs = Ks + C::TILE;
         f32x16_t s[BKV / 32];
 #pragma unroll
         for (int mt = 0; mt < BKV / 32; ++mt)
 #pragma unroll
             for (int e = 0; e < 16; ++e) s[mt][e] = 0.0f;
+        // all K fragments of the tile first, so LDS latency hides under MFMAs
+        bf16x8_t kf[D / 16][BKV / 32];
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
+        for (int ks = 0; ks < D / 16; ++ks)
 #pragma unroll
-            for (int mt = 0; mt < BKV / 32; ++mt) {
-                const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
+            for (int mt = 0; mt < BKV / 32; ++mt)
+                kf[ks][mt] = *reinterpret_cast<const bf16x8_t*>(
                     Ks + k_off(mt * 32 + col, 2 * ks + g, C::ROW));
-                s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[mt], 0, 0, 0);
-            }
-        }
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+            for (int mt = 0; mt < BKV / 32; ++mt)
+                s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks][mt], qf[ks], s[mt], 0, 0, 0);
         // masks: keys past S, and (causal) keys after this lane's query
         const bool need_mask = (k0 + BKV > S) || (CAUSAL && k0 + BKV - 1 > qw0);
         if (need_mask) {
@@ -260,12 +267,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
     };
 
     if (n_kv > 0) {
-        dma(0, 0);
+        dma(k_s0, v_s0, 0);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA writes have landed
         __syncthreads();
-        for (int j = 0; j < n_kv; ++j) {
-            if (j + 1 < n_kv) dma((j + 1) & 1, (j + 1) * BKV);
-            compute(j & 1, j * BKV);
+        for (int j = 0; j < n_kv; j += 2) {
+            if (j + 1 < n_kv) dma(k_s1, v_s1, (j + 1) * BKV);
+            compute(k_s0, v_s0, j * BKV);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (j + 1 >= n_kv) break;
+            if (j + 2 < n_kv) dma(k_s0, v_s0, (j + 2) * BKV);
+            compute(k_s1, v_s1, (j + 1) * BKV);
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
