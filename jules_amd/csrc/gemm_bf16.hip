@@ -204,15 +204,203 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Full-tile kernel (M % 256 == 0, N % 256 == 0, K % 64 == 0): both operand
+// tiles are copied HBM -> LDS by the LDS DMA path (global_load_lds_dwordx4,
+// each lane's 16 bytes land at base + 16 * lane) with no register staging.
+//   A: [256 rows][64 k], the same XOR-swizzled layout as above; each lane's
+//      source address is chosen so that the data lands swizzled.
+//   B: kept row-major [64 k][256 n] (512-byte rows), 8-byte chunk c of row r
+//      at c ^ (4 * (r & 3)); the MFMA B operand (8 consecutive k of one n per
+//      lane) comes from two ds_read_b64_tr_b16: in each 16-lane group lane s
+//      addresses row rb + s/4, chunk cb + s%4, and lane i receives
+//      B[rb + k][4 cb + i] for k = 0..3.
+// The DMA of slice k+1 is issued before the MFMAs of slice k and waited for
+// (vmcnt(0) + barrier) after them.  A partial K tile cannot be zero-filled by
+// the DMA copy; other shapes use the register-staged kernel above.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+// ds_read_b64_tr_b16 issued as inline asm.  Through the builtin, the
+// compiler's wait-count pass assumes the read may alias any LDS DMA still in
+// flight and inserts a full vmcnt(0) wait before it, which serialises the DMA
+// of the next slice with the compute of this one.  As asm the read is not
+// tracked: the caller must wait on lgkmcnt itself (lgkm_fence below) before
+// using the result, and must only read a stage whose DMA has completed (the
+// vmcnt(0) + barrier at the end of every slice).
+__device__ __forceinline__ u32x2_t ds_read_tr16_b64(const uint8_t* lds_ptr) {
+    u32x2_t v;
+    const uint32_t a = (uint32_t)(uintptr_t)lds_ptr;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(a) : "memory");
+    return v;
+}
+__device__ __forceinline__ u32x4_t ds_read_b128_asm(const uint8_t* lds_ptr) {
+    u32x4_t v;
+    const uint32_t a = (uint32_t)(uintptr_t)lds_ptr;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
+    return v;
+}
+
+// One k-step's MFMA operands: 4 A fragments (one ds_read_b128 each) and 4 B
+// fragments (two ds_read_b64_tr_b16 each) = 12 LDS reads.
+struct Frags {
+    u32x4_t a[4];
+    u32x4_t b[4];
+};
+
+// Waits until at most N LDS reads are outstanding.  LDS reads complete in
+// issue order, so with the 12 reads of the next k-step issued after this
+// one's, lgkmcnt(12) means this k-step's operands have arrived.  The operands
+// pass through the asm so no MFMA that uses them is scheduled before it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(Frags& f) {
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.a[2]), "+v"(f.a[3]), "+v"(f.b[0]),
+                   "+v"(f.b[1]), "+v"(f.b[2]), "+v"(f.b[3])
+                 : "n"(N)
+                 : "memory");
+}
+
+template <int ACT>
+__global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+    const float* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(1024))) uint8_t sm[2 * STAGE_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    // ---- XCD-aware tile order (see gemm_bf16_kernel) ----
+    const int tiles_m = M / BM, tiles_n = N / BN;
+    const int nblk = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if ((nblk & 7) == 0) t = (t & 7) * (nblk >> 3) + (t >> 3);
+    constexpr int GM = 4;
+    const int group = t / (GM * tiles_n);
+    const int first_m = group * GM;
+    const int gsize = min(GM, tiles_m - first_m);
+    const int tile_m = first_m + (t % (GM * tiles_n)) % gsize;
+    const int tile_n = (t % (GM * tiles_n)) / gsize;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+    auto dma = [&](uint8_t* As, uint8_t* Bs, int k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // A: 32 segments of 8 rows x 128 B
+            const int seg = i * 4 + wave;
+            const int row = seg * 8 + (lane >> 3);
+            const int lc = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+            __builtin_amdgcn_global_load_lds(A + (int64_t)(m0 + row) * K + k0 + 8 * lc,
+                                             (lds_void*)(As + seg * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // B: 32 segments of 2 rows x 512 B
+            const int seg = i * 4 + wave;
+            const int r = seg * 2 + (lane >> 5);
+            const int lu = (lane & 31) ^ (2 * (r & 3));
+            __builtin_amdgcn_global_load_lds(B + (int64_t)(k0 + r) * N + n0 + 8 * lu,
+                                             (lds_void*)(Bs + seg * 1024), 16, 0, 0);
+        }
+    };
+
+    f32x16_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int wm = wave >> 1, wn = wave & 1;
+    const int frag_row = lane & 31;
+    const int frag_half = lane >> 5;
+    const int ts = lane & 15, tdh = (lane >> 4) & 1;
+
+    auto issue = [&](Frags& f, const uint8_t* As, const uint8_t* Bs, int ks) {
+        const int chunk = ks * 2 + frag_half;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            f.a[mt] = ds_read_b128_asm(As + swz(wm * 128 + mt * 32 + frag_row, chunk));
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const int c8 = (wn * 128 + nt * 32 + 16 * tdh) / 4 + (ts & 3);
+            const int r0 = 16 * ks + 8 * frag_half + (ts >> 2);
+            const u32x2_t lo = ds_read_tr16_b64(Bs + r0 * 512 + ((c8 ^ (4 * (r0 & 3))) << 3));
+            const u32x2_t hi =
+                ds_read_tr16_b64(Bs + (r0 + 4) * 512 + ((c8 ^ (4 * ((r0 + 4) & 3))) << 3));
+            f.b[nt] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        }
+    };
+    auto mfmas = [&](const Frags& f) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8_t, f.a[mt]), __builtin_bit_cast(bf16x8_t, f.b[nt]),
+                    acc[mt][nt], 0, 0, 0);
+    };
+    // software-pipelined k-steps: operands of step ks+1 are read while the
+    // MFMAs of step ks run
+    auto compute = [&](const uint8_t* As, const uint8_t* Bs) {
+        Frags f0, f1;
+        issue(f0, As, Bs, 0);
+        issue(f1, As, Bs, 1);
+        lgkm_wait<12>(f0);
+        mfmas(f0);
+        issue(f0, As, Bs, 2);
+        lgkm_wait<12>(f1);
+        mfmas(f1);
+        issue(f1, As, Bs, 3);
+        lgkm_wait<12>(f0);
+        mfmas(f0);
+        lgkm_wait<0>(f1);
+        mfmas(f1);
+    };
+
+    const int KT = K / BK;
+    dma(sm, sm + TILE_BYTES, 0);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA writes have landed
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        uint8_t* cur = sm + (kt & 1) * STAGE_BYTES;
+        uint8_t* nxt = sm + ((kt + 1) & 1) * STAGE_BYTES;
+        if (kt + 1 < KT) dma(nxt, nxt + TILE_BYTES, (kt + 1) * BK);
+        compute(cur, cur + TILE_BYTES);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const int col = n0 + wn * 128 + nt * 32 + frag_row;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm * 128 + mt * 32 + 8 * (e >> 2) + 4 * frag_half + (e & 3);
+                const float v = act_bf16<ACT>(acc[mt][nt][e] + bv);
+                C[(int64_t)row * N + col] = __builtin_bit_cast(uint16_t, (__bf16)v);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gemm_bf16(int act, const uint16_t* A, const uint16_t* B, const float* bias,
                             uint16_t* C, int M, int N, int K, hipStream_t s) {
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const bool full = M % BM == 0 && N % BN == 0 && K % BK == 0 && K > 0;
     hipError_t e = hipSuccess;
     JH_DISPATCH_ACT(act, ACT, {
-        hipLaunchKernelGGL(gemm_bf16_kernel<ACT>, dim3(tiles), dim3(THREADS), 0, s, A, B, bias,
-                           C, M, N, K);
+        if (full)
+            hipLaunchKernelGGL(gemm_bf16_dma_kernel<ACT>, dim3(tiles), dim3(THREADS), 0, s, A, B,
+                               bias, C, M, N, K);
+        else
+            hipLaunchKernelGGL(gemm_bf16_kernel<ACT>, dim3(tiles), dim3(THREADS), 0, s, A, B, bias,
+                               C, M, N, K);
         e = hipGetLastError();
     });
     return e;
