@@ -26,6 +26,8 @@
 // XCDs (round robin over 8), so ids are remapped so that each XCD's workgroups
 // cover a compact 4-row band of output tiles that shares A and B slices in
 // that XCD's L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -205,29 +207,42 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Full-tile kernel (M % 256 == 0, N % 256 == 0, K % 64 == 0): both operand
-// tiles are copied HBM -> LDS by the LDS DMA path (global_load_lds_dwordx4,
-// each lane's 16 bytes land at base + 16 * lane) with no register staging.
-//   A: [256 rows][64 k], the same XOR-swizzled layout as above; each lane's
-//      source address is chosen so that the data lands swizzled.
-//   B: kept row-major [64 k][256 n] (512-byte rows), 8-byte chunk c of row r
-//      at c ^ (4 * (r & 3)); the MFMA B operand (8 consecutive k of one n per
-//      lane) comes from two ds_read_b64_tr_b16: in each 16-lane group lane s
-//      addresses row rb + s/4, chunk cb + s%4, and lane i receives
+// Full-tile kernel (M % 256 == 0, N % 256 == 0, K % 32 == 0).
+//
+// Both operand tiles are copied HBM -> LDS by the LDS DMA path
+// (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16 * lane),
+// with no register staging, through a ring of 4 stages of 32 k each
+// (4 x 32 KiB): the copy of slice k+3 is issued while slice k is computed, so
+// a copy has three slices of MFMA time to land.
+//   A stage: [256 rows][32 k] (64-byte rows), 16-byte chunk c of row r at
+//      c ^ ((r >> 2) & 3): the fragment read (16 consecutive rows, one chunk)
+//      touches 16 distinct bank slots.  Each lane's DMA source address is
+//      chosen so the data lands swizzled.
+//   B stage: row-major [32 k][256 n] (512-byte rows), 8-byte chunk c of row r
+//      at c ^ (4 * (r & 3)).  The MFMA B operand (8 consecutive k of one n
+//      per lane) comes from two ds_read_b64_tr_b16: in each 16-lane group
+//      lane s addresses row rb + s/4, chunk cb + s%4, and lane i receives
 //      B[rb + k][4 cb + i] for k = 0..3.
-// The DMA of slice k+1 is issued before the MFMAs of slice k and waited for
-// (vmcnt(0) + barrier) after them.  A partial K tile cannot be zero-filled by
-// the DMA copy; other shapes use the register-staged kernel above.
+// A partial K slice cannot be zero-filled by the DMA copy; other shapes use
+// the register-staged kernel above.
 // ---------------------------------------------------------------------------
+constexpr int DBK = 32;                   // k per stage
+constexpr int NSTAGE = 4;
+constexpr int DTILE = 256 * DBK * 2;      // one operand stage: 16 KiB
+constexpr int DSTAGE = 2 * DTILE;         // A then B
+
 typedef __attribute__((address_space(3))) void lds_void;
 
-// ds_read_b64_tr_b16 issued as inline asm.  Through the builtin, the
-// compiler's wait-count pass assumes the read may alias any LDS DMA still in
-// flight and inserts a full vmcnt(0) wait before it, which serialises the DMA
-// of the next slice with the compute of this one.  As asm the read is not
-// tracked: the caller must wait on lgkmcnt itself (lgkm_fence below) before
-// using the result, and must only read a stage whose DMA has completed (the
-// vmcnt(0) + barrier at the end of every slice).
+__device__ __forceinline__ int swz_a32(int row, int chunk) {
+    return row * (DBK * 2) + ((chunk ^ ((row >> 2) & 3)) << 4);
+}
+
+// LDS reads issued as inline asm.  Through the builtins, the compiler's
+// wait-count pass assumes a transposed read may alias any LDS DMA still in
+// flight and inserts a full vmcnt(0) wait before it, serialising the copies
+// with the compute.  As asm the reads are not tracked: the code below waits
+// on lgkmcnt itself before using a result (lgkm_wait), and reads only stages
+// whose copies have completed (vmcnt wait + barrier at the top of a slice).
 __device__ __forceinline__ u32x2_t ds_read_tr16_b64(const uint8_t* lds_ptr) {
     u32x2_t v;
     const uint32_t a = (uint32_t)(uintptr_t)lds_ptr;
@@ -265,7 +280,7 @@ template <int ACT>
 __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     const float* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K) {
-    __shared__ __attribute__((aligned(1024))) uint8_t sm[2 * STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sm[NSTAGE * DSTAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -284,23 +299,36 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
     const int tile_n = (t % (GM * tiles_n)) / gsize;
     const int m0 = tile_m * BM, n0 = tile_n * BN;
 
-    auto dma = [&](uint8_t* As, uint8_t* Bs, int k0) {
+    // wave index as a scalar: the LDS destinations of the copies (M0) and
+    // their segment offsets are then computed on the scalar unit
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+
+    // ---- copy of one slice: 16 A segments (16 rows x 64 B) and 16 B segments
+    // (2 rows x 512 B) of 1 KiB; wave w moves segments w, w+4, w+8, w+12.
+    // Piece q (0..7) is one global_load_lds instruction: q < 4 an A segment,
+    // else a B segment. ----
+    const uint16_t* a_src[4];
+    const uint16_t* b_src[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {  // A: 32 segments of 8 rows x 128 B
-            const int seg = i * 4 + wave;
-            const int row = seg * 8 + (lane >> 3);
-            const int lc = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
-            __builtin_amdgcn_global_load_lds(A + (int64_t)(m0 + row) * K + k0 + 8 * lc,
-                                             (lds_void*)(As + seg * 1024), 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {  // B: 32 segments of 2 rows x 512 B
-            const int seg = i * 4 + wave;
-            const int r = seg * 2 + (lane >> 5);
-            const int lu = (lane & 31) ^ (2 * (r & 3));
-            __builtin_amdgcn_global_load_lds(B + (int64_t)(k0 + r) * N + n0 + 8 * lu,
-                                             (lds_void*)(Bs + seg * 1024), 16, 0, 0);
-        }
+    for (int i = 0; i < 4; ++i) {
+        const int seg = i * 4 + wave_s;
+        const int row = seg * 16 + (lane >> 2);
+        const int lc = (lane & 3) ^ ((row >> 2) & 3);
+        a_src[i] = A + (int64_t)(m0 + row) * K + 8 * lc;
+        const int r = seg * 2 + (lane >> 5);
+        const int lu = (lane & 31) ^ (2 * (r & 3));
+        b_src[i] = B + (int64_t)r * N + n0 + 8 * lu;
+    }
+    auto dma_piece = [&](int stage, int kt, int q) {
+        uint8_t* As = sm + stage * DSTAGE;
+        const int i = q & 3;
+        const int seg = i * 4 + wave_s;
+        if (q < 4)
+            __builtin_amdgcn_global_load_lds(a_src[i] + kt * DBK, (lds_void*)(As + seg * 1024), 16,
+                                             0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(b_src[i] + (int64_t)kt * DBK * N,
+                                             (lds_void*)(As + DTILE + seg * 1024), 16, 0, 0);
     };
 
     f32x16_t acc[4][4];
@@ -316,60 +344,117 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
     const int frag_half = lane >> 5;
     const int ts = lane & 15, tdh = (lane >> 4) & 1;
 
-    auto issue = [&](Frags& f, const uint8_t* As, const uint8_t* Bs, int ks) {
-        const int chunk = ks * 2 + frag_half;
+    // LDS byte offsets (within a stage) of the 12 reads of one k-step; the
+    // k-step adds 32 bytes to the A offsets (two 16-byte chunks, applied
+    // before the swizzle) and 16 rows to the B offsets.
+    // Piece p (0..11): p < 4 the A fragment of m-tile p (one ds_read_b128);
+    // p = 4 + 2 nt + h the half h of the B fragment of n-tile nt.
+    auto piece_addr = [&](int ks, int p) -> int {
+        if (p < 4) return swz_a32(wm * 128 + p * 32 + frag_row, ks * 2 + frag_half);
+        const int nt = (p - 4) >> 1, h = (p - 4) & 1;
+        const int c8 = (wn * 128 + nt * 32 + 16 * tdh) / 4 + (ts & 3);
+        const int r0 = 16 * ks + 8 * frag_half + (ts >> 2) + 4 * h;
+        return DTILE + r0 * 512 + ((c8 ^ (4 * (r0 & 3))) << 3);
+    };
+    int off[2][12];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            f.a[mt] = ds_read_b128_asm(As + swz(wm * 128 + mt * 32 + frag_row, chunk));
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-            const int c8 = (wn * 128 + nt * 32 + 16 * tdh) / 4 + (ts & 3);
-            const int r0 = 16 * ks + 8 * frag_half + (ts >> 2);
-            const u32x2_t lo = ds_read_tr16_b64(Bs + r0 * 512 + ((c8 ^ (4 * (r0 & 3))) << 3));
-            const u32x2_t hi =
-                ds_read_tr16_b64(Bs + (r0 + 4) * 512 + ((c8 ^ (4 * ((r0 + 4) & 3))) << 3));
-            f.b[nt] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+        for (int p = 0; p < 12; ++p) off[ks][p] = piece_addr(ks, p);
+
+    auto read_piece = [&](Frags& f, const uint8_t* stage_base, int ks, int p) {
+        const uint8_t* ptr = stage_base + off[ks][p];
+        if (p < 4) {
+            f.a[p] = ds_read_b128_asm(ptr);
+        } else {
+            const int nt = (p - 4) >> 1;
+            const u32x2_t v = ds_read_tr16_b64(ptr);
+            if ((p & 1) == 0) {
+                f.b[nt][0] = v[0];
+                f.b[nt][1] = v[1];
+            } else {
+                f.b[nt][2] = v[0];
+                f.b[nt][3] = v[1];
+            }
         }
     };
-    auto mfmas = [&](const Frags& f) {
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt)
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    __builtin_bit_cast(bf16x8_t, f.a[mt]), __builtin_bit_cast(bf16x8_t, f.b[nt]),
-                    acc[mt][nt], 0, 0, 0);
-    };
-    // software-pipelined k-steps: operands of step ks+1 are read while the
-    // MFMAs of step ks run
-    auto compute = [&](const uint8_t* As, const uint8_t* Bs) {
-        Frags f0, f1;
-        issue(f0, As, Bs, 0);
-        issue(f1, As, Bs, 1);
-        lgkm_wait<12>(f0);
-        mfmas(f0);
-        issue(f0, As, Bs, 2);
-        lgkm_wait<12>(f1);
-        mfmas(f1);
-        issue(f1, As, Bs, 3);
-        lgkm_wait<12>(f0);
-        mfmas(f0);
-        lgkm_wait<0>(f1);
-        mfmas(f1);
+    auto mfma1 = [&](const Frags& f, int i) {
+        const int mt = i >> 2, nt = i & 3;
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, f.a[mt]), __builtin_bit_cast(bf16x8_t, f.b[nt]),
+            acc[mt][nt], 0, 0, 0);
     };
 
-    const int KT = K / BK;
-    dma(sm, sm + TILE_BYTES, 0);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA writes have landed
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        uint8_t* cur = sm + (kt & 1) * STAGE_BYTES;
-        uint8_t* nxt = sm + ((kt + 1) & 1) * STAGE_BYTES;
-        if (kt + 1 < KT) dma(nxt, nxt + TILE_BYTES, (kt + 1) * BK);
-        compute(cur, cur + TILE_BYTES);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-    }
+    // Software pipeline over k-steps of 16.  Each MFMA (32 cycles) is followed
+    // by at most two other instructions' worth of work - an LDS read of the
+    // next k-step's operands and/or one copy instruction of a later slice -
+    // so they issue while the matrix core is busy instead of between groups
+    // of MFMAs.  sched_barrier(0) pins this order (the scheduler would
+    // otherwise cluster the reads and copies).
+    //   k-step 0 of slice kt: MFMAs on f0, reads of k-step 1 into f1.
+    //   k-step 1 of slice kt: wait for slice kt+1 (vmcnt + barrier), MFMAs on
+    //     f1, the 8 copies of slice kt+4 into stage kt%4 (read by every wave
+    //     before the barrier) and the reads of slice kt+1's k-step 0 into f0.
+    const int KT = K / DBK;
+    auto wait_slice = [&](int kt, int last_issued) {
+        // this wave's copies of slice kt have landed once at most the copies
+        // of the later slices already issued (8 instructions each) are
+        // outstanding
+        const int later = last_issued - kt;
+        if (later >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        else if (later == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // A bare s_barrier: __syncthreads() adds a workgroup fence whose wait
+        // drains all of this wave's copies (vmcnt(0)).  The waits and the
+        // LDS-read asm carry "memory" clobbers, so the compiler keeps copies
+        // and reads on their side of the barrier.
+        __builtin_amdgcn_s_barrier();
+    };
+    Frags fr[2];
+    auto slice = [&](int kt, auto with_dma, auto with_next) {
+        const uint8_t* cur = sm + (kt % NSTAGE) * DSTAGE;
+        Frags& f0 = fr[0];
+        Frags& f1 = fr[1];
+        lgkm_wait<0>(f0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            mfma1(f0, i);
+            if (i < 12) read_piece(f1, cur, 1, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        lgkm_wait<0>(f1);
+        mfma1(f1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // slices issued so far: 0..3 and kt'+4 for every earlier kt'
+        if constexpr (decltype(with_next)::value) wait_slice(kt + 1, min(KT - 1, kt + NSTAGE - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* nxt = sm + ((kt + 1) % NSTAGE) * DSTAGE;
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+            mfma1(f1, i);
+            if constexpr (decltype(with_dma)::value)
+                if (i <= 8) dma_piece(kt % NSTAGE, kt + NSTAGE, i - 1);
+            if constexpr (decltype(with_next)::value)
+                if (i <= 12) read_piece(f0, nxt, 0, i - 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+#pragma unroll
+    for (int p = 0; p < NSTAGE; ++p)
+        if (p < KT)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) dma_piece(p, p, q);
+    wait_slice(0, min(KT - 1, NSTAGE - 1));
+#pragma unroll
+    for (int p = 0; p < 12; ++p) read_piece(fr[0], sm, 0, p);
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    int kt = 0;
+    for (; kt + NSTAGE < KT; ++kt) slice(kt, yes{}, yes{});
+    for (; kt + 1 < KT; ++kt) slice(kt, no{}, yes{});
+    slice(kt, no{}, no{});
 
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
@@ -392,7 +477,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
 hipError_t launch_gemm_bf16(int act, const uint16_t* A, const uint16_t* B, const float* bias,
                             uint16_t* C, int M, int N, int K, hipStream_t s) {
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    const bool full = M % BM == 0 && N % BN == 0 && K % BK == 0 && K > 0;
+    const bool full = M % BM == 0 && N % BN == 0 && K % DBK == 0 && K > 0;
     hipError_t e = hipSuccess;
     JH_DISPATCH_ACT(act, ACT, {
         if (full)
