@@ -212,17 +212,21 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_kernel(
 // Both operand tiles are copied HBM -> LDS by the LDS DMA path
 // (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16 * lane),
 // with no register staging, through a ring of 4 stages of 32 k each
-// (4 x 32 KiB): the copy of slice k+3 is issued while slice k is computed, so
-// a copy has three slices of MFMA time to land.
+// (4 x 32 KiB): the copy of slice k+3 is spread over the computation of
+// slice k, so a copy has two to three slices of MFMA time to land.
+// The LDS has 64 banks of 4 bytes (256 bytes per clock); a ds_read_b128
+// serves 16 lanes per clock, a ds_read_b64_tr_b16 32 lanes.
 //   A stage: [256 rows][32 k] (64-byte rows), 16-byte chunk c of row r at
 //      c ^ ((r >> 2) & 3): the fragment read (16 consecutive rows, one chunk)
-//      touches 16 distinct bank slots.  Each lane's DMA source address is
-//      chosen so the data lands swizzled.
-//   B stage: row-major [32 k][256 n] (512-byte rows), 8-byte chunk c of row r
-//      at c ^ (4 * (r & 3)).  The MFMA B operand (8 consecutive k of one n
-//      per lane) comes from two ds_read_b64_tr_b16: in each 16-lane group
-//      lane s addresses row rb + s/4, chunk cb + s%4, and lane i receives
-//      B[rb + k][4 cb + i] for k = 0..3.
+//      touches 16 distinct 16-byte bank groups.  Each lane's DMA source
+//      address is chosen so the data lands swizzled.
+//   B stage: row-major [32 k][256 n] (512-byte rows), 32-byte block b of
+//      row r at b ^ (2 * (r & 3)).  The MFMA B operand (8 consecutive k of
+//      one n per lane) comes from two ds_read_b64_tr_b16: in each 16-lane
+//      group lane s addresses row rb + s/4, 8-byte chunk cb + s%4, and lane i
+//      receives B[rb + k][4 cb + i] for k = 0..3.  The two 16-lane groups
+//      served together read blocks b and b+1 (b even) of the same 4 rows; the
+//      swizzle spreads those 8 reads over all 8 blocks of a 256-byte window.
 // A partial K slice cannot be zero-filled by the DMA copy; other shapes use
 // the register-staged kernel above.
 // ---------------------------------------------------------------------------
@@ -316,7 +320,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
         const int lc = (lane & 3) ^ ((row >> 2) & 3);
         a_src[i] = A + (int64_t)(m0 + row) * K + 8 * lc;
         const int r = seg * 2 + (lane >> 5);
-        const int lu = (lane & 31) ^ (2 * (r & 3));
+        const int lu = (lane & 31) ^ (4 * (r & 3));  // 16-byte units: block ^ 2 (r & 3)
         b_src[i] = B + (int64_t)r * N + n0 + 8 * lu;
     }
     auto dma_piece = [&](int stage, int kt, int q) {
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
         const int nt = (p - 4) >> 1, h = (p - 4) & 1;
         const int c8 = (wn * 128 + nt * 32 + 16 * tdh) / 4 + (ts & 3);
         const int r0 = 16 * ks + 8 * frag_half + (ts >> 2) + 4 * h;
-        return DTILE + r0 * 512 + ((c8 ^ (4 * (r0 & 3))) << 3);
+        return DTILE + r0 * 512 + ((c8 ^ (8 * (r0 & 3))) << 3);
     };
     int off[2][12];
 #pragma unroll
@@ -386,24 +390,27 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
     };
 
     // Software pipeline over k-steps of 16.  Each MFMA (32 cycles) is followed
-    // by at most two other instructions' worth of work - an LDS read of the
-    // next k-step's operands and/or one copy instruction of a later slice -
-    // so they issue while the matrix core is busy instead of between groups
-    // of MFMAs.  sched_barrier(0) pins this order (the scheduler would
-    // otherwise cluster the reads and copies).
-    //   k-step 0 of slice kt: MFMAs on f0, reads of k-step 1 into f1.
+    // by at most one LDS read of the next k-step's operands and, every fourth
+    // MFMA, one copy instruction of a later slice, so they issue while the
+    // matrix core is busy instead of between groups of MFMAs.  Spreading the
+    // copies matters: the four waves' 32 copies of a slice move 32 KiB through
+    // the vector memory path (64 bytes per clock), and a burst of them stalls
+    // the issuing waves, MFMAs included.  sched_barrier(0) pins this order
+    // (the scheduler would otherwise cluster the reads and copies).
+    //   k-step 0 of slice kt: MFMAs on f0, reads of k-step 1 into f1, copies
+    //     0-3 of slice kt+3 into stage (kt+3)%4.
     //   k-step 1 of slice kt: wait for slice kt+1 (vmcnt + barrier), MFMAs on
-    //     f1, the 8 copies of slice kt+4 into stage kt%4 (read by every wave
-    //     before the barrier) and the reads of slice kt+1's k-step 0 into f0.
+    //     f1, copies 4-7 of slice kt+3 and the reads of slice kt+1's k-step 0
+    //     into f0.
+    // Stage (kt+3)%4 = (kt-1)%4 was last read in k-step 0 of slice kt-1, and
+    // every wave passed the barrier of slice kt-1 after those reads completed.
     const int KT = K / DBK;
-    auto wait_slice = [&](int kt, int last_issued) {
-        // this wave's copies of slice kt have landed once at most the copies
-        // of the later slices already issued (8 instructions each) are
-        // outstanding
-        const int later = last_issued - kt;
-        if (later >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
-        else if (later == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-        else if (later == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    auto wait_slice = [&](int kt, int outstanding) {
+        // this wave's copies of slice kt have landed once at most the
+        // `outstanding` copy instructions issued after them remain
+        if (outstanding >= 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (outstanding >= 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        else if (outstanding >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         // A bare s_barrier: __syncthreads() adds a workgroup fence whose wait
         // drains all of this wave's copies (vmcnt(0)).  The waits and the
@@ -413,7 +420,10 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
     };
     Frags fr[2];
     auto slice = [&](int kt, auto with_dma, auto with_next) {
+        constexpr bool DMA = decltype(with_dma)::value;
+        constexpr bool NEXT = decltype(with_next)::value;
         const uint8_t* cur = sm + (kt % NSTAGE) * DSTAGE;
+        const int dst = (kt + NSTAGE - 1) % NSTAGE;
         Frags& f0 = fr[0];
         Frags& f1 = fr[1];
         lgkm_wait<0>(f0);
@@ -421,38 +431,44 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
         for (int i = 0; i < 16; ++i) {
             mfma1(f0, i);
             if (i < 12) read_piece(f1, cur, 1, i);
+            if constexpr (DMA)
+                if ((i & 3) == 1) dma_piece(dst, kt + NSTAGE - 1, i >> 2);
             __builtin_amdgcn_sched_barrier(0);
         }
         lgkm_wait<0>(f1);
         mfma1(f1, 0);
         __builtin_amdgcn_sched_barrier(0);
-        // slices issued so far: 0..3 and kt'+4 for every earlier kt'
-        if constexpr (decltype(with_next)::value) wait_slice(kt + 1, min(KT - 1, kt + NSTAGE - 1));
+        if constexpr (NEXT) {
+            // issued after slice kt+1: slice kt+2 if it exists (8), and the
+            // first half of slice kt+3 (4)
+            wait_slice(kt + 1, (kt + 2 < KT ? 8 : 0) + (DMA ? 4 : 0));
+        }
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* nxt = sm + ((kt + 1) % NSTAGE) * DSTAGE;
 #pragma unroll
         for (int i = 1; i < 16; ++i) {
             mfma1(f1, i);
-            if constexpr (decltype(with_dma)::value)
-                if (i <= 8) dma_piece(kt % NSTAGE, kt + NSTAGE, i - 1);
-            if constexpr (decltype(with_next)::value)
+            if constexpr (NEXT)
                 if (i <= 12) read_piece(f0, nxt, 0, i - 1);
+            if constexpr (DMA)
+                if ((i & 3) == 3) dma_piece(dst, kt + NSTAGE - 1, 4 + (i >> 2));
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
+    // prologue: slices 0..2 into stages 0..2 (stage 3 is filled during slice 0)
 #pragma unroll
-    for (int p = 0; p < NSTAGE; ++p)
+    for (int p = 0; p < NSTAGE - 1; ++p)
         if (p < KT)
 #pragma unroll
             for (int q = 0; q < 8; ++q) dma_piece(p, p, q);
-    wait_slice(0, min(KT - 1, NSTAGE - 1));
+    wait_slice(0, 8 * (min(KT - 1, NSTAGE - 2)));
 #pragma unroll
     for (int p = 0; p < 12; ++p) read_piece(fr[0], sm, 0, p);
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
     int kt = 0;
-    for (; kt + NSTAGE < KT; ++kt) slice(kt, yes{}, yes{});
+    for (; kt + NSTAGE - 1 < KT; ++kt) slice(kt, yes{}, yes{});
     for (; kt + 1 < KT; ++kt) slice(kt, no{}, yes{});
     slice(kt, no{}, no{});
 
