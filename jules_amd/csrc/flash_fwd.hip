@@ -33,6 +33,8 @@
 // bf16: v_mfma_f32_32x32x16_bf16, fp32 softmax statistics, exp2 with
 // scale*log2(e) folded into one fma.  fp32: v_mfma_f32_32x32x2_f32 (full fp32
 // products), same recurrence.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -52,7 +54,7 @@ __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); 
 // XCD runs at once then span about two heads, whose K and V (2 MiB each at
 // S=4096, D=128) stay in that XCD's 4 MiB L2 instead of being re-read from
 // HBM by every query tile.
-__device__ __forceinline__ void block_coords(int BH, int nq, int* bh, int* q0) {
+__device__ __forceinline__ void block_coords(int BH, int nq, int bq, int* bh, int* q0) {
     const int b = blockIdx.x;
     int head, qi;
     if ((BH & 7) == 0) {
@@ -64,232 +66,454 @@ __device__ __forceinline__ void block_coords(int BH, int nq, int* bh, int* q0) {
         qi = b % nq;
     }
     *bh = head;
-    *q0 = (nq - 1 - qi) * BQ;
-}
-
-__device__ __forceinline__ bf16x8_t pack8(const float* p) {
-    u32x4_t u;
-    u[0] = pack_bf16x2(p[0], p[1]);
-    u[1] = pack_bf16x2(p[2], p[3]);
-    u[2] = pack_bf16x2(p[4], p[5]);
-    u[3] = pack_bf16x2(p[6], p[7]);
-    return __builtin_bit_cast(bf16x8_t, u);
+    *q0 = (nq - 1 - qi) * bq;
 }
 
 // ---------------------------------------------------------------------------
 // bf16
 //
-// K and V tiles are copied HBM -> LDS by the LDS DMA path
-// (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16 * lane),
-// with no register staging; the source address of every lane is permuted so
-// the data lands in the swizzled layout below.  Both tiles are row-major
-// [key][d] (D*2 bytes per row):
-//   K: 16-byte unit u of row r at unit u ^ (r & 7).  The S^T A operand (one
-//      key row, 8 consecutive d per lane) is one ds_read_b128; 8 consecutive
-//      rows hit distinct bank groups.
-//   V: 8-byte chunk c of row r at chunk c ^ (4 * (r & 3)).  The V^T A operand
-//      (8 keys of one d per lane) comes from two ds_read_b64_tr_b16: in each
-//      16-lane group, lane s addresses row rb + s/4, chunk cb + s%4, and lane
-//      i receives V[rb + k][4 cb + i] for k = 0..3.  The swizzle makes the 16
-//      addresses of a group fall in 16 distinct chunks.
+// Workgroup: 8 waves x 32 queries = 256 query rows, two waves per SIMD (up to
+// 256 registers each).  The waves form two groups, A = waves 0-3 and B =
+// waves 4-7, one wave of each per SIMD, run half a tile out of phase.  Phase
+// p ends with a barrier of all 8 waves; in each phase one group issues MFMAs
+// while the other runs the softmax on the vector ALU, so the SIMD's matrix
+// core and vector ALU work at the same time (they co-issue across waves):
+//   MFMA(j):    S_j = K_j Q^T (this wave's 32 queries x 64 keys) and
+//               O^T += V_{j-1}^T P_{j-1}^T;
+//   SOFTMAX(j): row max of S_j, running-max update (acc *= alpha when it
+//               moved), P_j = exp2(S_j c - m) packed to bf16, row sums.
+//   group A: MFMA(j) in phase 2j,     SOFTMAX(j) in phase 2j+1;
+//   group B: MFMA(j) in phase 2j+1,   SOFTMAX(j) in phase 2j+2.
+//
+// K and V tiles of 64 keys go HBM -> LDS by the LDS DMA path
+// (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16 * lane)
+// through a ring of 4 stages; tile t lives in stage t % 4.  K_t is read in
+// phases 2t and 2t+1, V_t in phases 2t+2 and 2t+3, so tile t+4 is copied in
+// phase 2t+4 (all 8 waves share the copy) and has until phase 2t+8 to land.
+// Each lane's source address is permuted so the data lands in the swizzled
+// layouts below (LDS: 64 banks of 4 bytes; a ds_read_b128 serves 16 lanes per
+// clock, a ds_read_b64_tr_b16 32 lanes).  Both tiles are row-major [key][d],
+// D*2 bytes per row:
+//   K: 16-byte unit u of row r at u ^ kswz(r).  The S^T A operand (one key
+//      row, 8 consecutive d per lane) is one ds_read_b128; the 16 rows a
+//      read serves per clock land in 16 distinct 16-byte bank groups.
+//   V: 8-byte chunk c of row r at c ^ vswz(r).  The V^T A operand (8 keys of
+//      one d per lane) comes from two ds_read_b64_tr_b16: in each 16-lane
+//      group lane s addresses row rb + s/4, chunk cb + s%4, and lane i
+//      receives V[rb + k][4 cb + i] for k = 0..3; the two groups served
+//      together read chunks cb..cb+7 of the same 4 rows, which the swizzle
+//      spreads over all 8 32-byte blocks of a 256-byte bank window.
+// The MFMA phase's LDS reads form one stream with a fixed look-ahead, so each
+// MFMA waits on a constant lgkmcnt.  The reads are inline asm: through the
+// builtins the compiler's wait-count pass assumes they may alias any LDS DMA
+// in flight and drains all copies (vmcnt(0)) first.
+//
 // Lazy rescale: the running max only moves when a tile's max exceeds it by
 // more than 8 (log2 units); p = exp2(s*c - m) then stays <= 256, exact in the
 // recurrence because the sum l uses the same m.
 // ---------------------------------------------------------------------------
+constexpr int BQ2 = 256;  // query rows per bf16 workgroup
+constexpr int NW2 = 8;    // waves per bf16 workgroup
+
 template <int D>
 struct Bf16Cfg {
     static constexpr int BKV = 64;
-    static constexpr int ROW = D * 2;                   // bytes per K / V row in LDS
-    static constexpr int TILE = BKV * ROW;              // one operand tile
-    static constexpr int STAGE = 2 * TILE;              // K then V
-    static constexpr int UNITS = ROW / 16;              // 16-byte units per row
-    static constexpr int NSEG = TILE / 1024;            // 1 KiB DMA segments per tile
+    static constexpr int ROW = D * 2;              // bytes per K / V row in LDS
+    static constexpr int TILE = BKV * ROW;         // one operand tile
+    static constexpr int STAGE = 2 * TILE;         // K then V
+    static constexpr int NSTAGE = 4;
+    static constexpr int UNITS = ROW / 16;         // 16-byte units per row
+    static constexpr int NSEG = TILE / 1024;       // 1 KiB DMA segments per operand tile
+    static constexpr int SEGW = NSEG / NW2;        // copy instructions per wave per operand tile
+    static constexpr int RPS = 1024 / ROW;         // rows per segment
+    static constexpr int KS = D / 16;              // k-steps of S^T = K Q^T
+    static constexpr int DT = D / 32;              // 32-row d tiles of O^T
+    static constexpr int NS = 2 * KS;              // MFMAs of one S tile (two 32-key halves)
+    static constexpr int NPV = 4 * DT;             // MFMAs of one PV product (four 16-key steps)
 };
 
-__device__ __forceinline__ int k_off(int row, int unit, int rowbytes) {
-    return row * rowbytes + ((unit ^ (row & 7)) << 4);
-}
-__device__ __forceinline__ int v_off(int row, int chunk8, int rowbytes) {
-    return row * rowbytes + ((chunk8 ^ (4 * (row & 3))) << 3);
-}
+// Order of the MFMAs of one MFMA phase: S and PV products alternate when
+// both are present.  MFMA m needs one LDS read (S: a K fragment) or two (PV:
+// the two halves of a V^T fragment), read in MFMA order.
+template <bool DO_S, bool DO_PV, int NS, int NPV>
+struct MfmaSeq {
+    static constexpr int NM = (DO_S ? NS : 0) + (DO_PV ? NPV : 0);
+    static constexpr bool is_s(int m) { return DO_S && (!DO_PV || (m % 2 == 0)); }
+    static constexpr int idx(int m) { return (DO_S && DO_PV) ? m / 2 : m; }
+    // reads of MFMAs 0..m
+    static constexpr int reads_upto(int m) {
+        int r = 0;
+        for (int k = 0; k <= m && k < NM; ++k) r += is_s(k) ? 1 : 2;
+        return r;
+    }
+    // the MFMA read r belongs to
+    static constexpr int owner(int r) {
+        int k = 0;
+        while (reads_upto(k) <= r) ++k;
+        return k;
+    }
+};
 
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+template <int D>
+__host__ __device__ constexpr int kswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+template <int D>
+__host__ __device__ constexpr int vswz(int r) { return D == 128 ? 8 * (r & 3) : 8 * ((r >> 1) & 1); }
+
 typedef __attribute__((address_space(3))) void lds_void;
 
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x4_t lds_b128(uint32_t addr) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2_t lds_tr16(uint32_t addr) {
+    u32x2_t v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+// Waits until at most N LDS reads are outstanding; the operand passes through
+// the asm so its consumer is not scheduled above the wait.
+template <int N, typename T>
+__device__ __forceinline__ void lgkm_wait(T& v) {
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N) : "memory");
+}
+template <int N, typename T>
+__device__ __forceinline__ void lgkm_wait2(T& a, T& b) {
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+__device__ __forceinline__ void vm_wait(int n) {
+    // n is one of the counts the copy schedule produces
+    if (n >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (n >= 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if (n >= 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+// A 16-byte global load the compiler's wait-count pass does not track; the
+// caller waits for it with an explicit vmcnt.
+__device__ __forceinline__ u32x4_t global_b128_untracked(const void* p) {
+    u32x4_t v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+// The value is redefined here: its uses stay after this point.
+__device__ __forceinline__ void reg_fence(u32x4_t& v) { asm volatile("" : "+v"(v)); }
+// Barrier of the workgroup without the fence __syncthreads() adds (whose wait
+// would drain every copy in flight).  The empty asm keeps the compiler from
+// moving copies or LDS reads across it, the sched_barriers keep the
+// scheduler from moving any other instruction across it: a phase's vector
+// work must stay in its phase.
+__device__ __forceinline__ void bare_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Lanes l and l ^ 32 exchange v: v_permlane32_swap swaps the upper 32 lanes
+// of its first operand with the lower 32 lanes of its second, so with both
+// holding v, a = {v[0..31], v[0..31]} and b = {v[32..63], v[32..63]}.  As asm
+// because the builtin's second result came back as a copy of the first.
+// s_nop 1: the VALU writes of the operands must be two wait states old.
+__device__ __forceinline__ void pair_swap(float v, float& a, float& b) {
+    a = v;
+    b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float pair_max(float v) {
+    float a, b;
+    pair_swap(v, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float pair_sum(float v) {
+    float a, b;
+    pair_swap(v, a, b);
+    return a + b;
+}
+
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
+__device__ __forceinline__ void flash_bf16_body(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ lse, int BH, int S,
     float c_log2) {
     using C = Bf16Cfg<D>;
     constexpr int BKV = C::BKV;
     constexpr float kLazy = 8.0f;
-    // One array per stage and operand, and the tile loop unrolled by two, so
-    // every LDS access names its array statically: the compiler can then see
-    // that reads of one stage never alias the DMA in flight into the other
-    // and does not wait for that DMA before reading.
-    __shared__ __attribute__((aligned(1024))) uint8_t k_s0[C::TILE];
-    __shared__ __attribute__((aligned(1024))) uint8_t v_s0[C::TILE];
-    __shared__ __attribute__((aligned(1024))) uint8_t k_s1[C::TILE];
-    __shared__ __attribute__((aligned(1024))) uint8_t v_s1[C::TILE];
+    constexpr int LA = 3;                       // MFMAs whose LDS reads are in flight
+    constexpr int KR = LA + 2, VR = LA + 2;     // K / V fragment ring sizes
+    constexpr int PIECES = 2 * C::SEGW;         // copy instructions per wave per tile
+    __shared__ __attribute__((aligned(1024))) uint8_t sm[C::NSTAGE * C::STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;  // 0: group A, 1: group B
     const int g = lane >> 5, col = lane & 31;
-    const int nq = (S + BQ - 1) / BQ;
+    const int nq = (S + BQ2 - 1) / BQ2;
     int bh, q0;
-    block_coords(BH, nq, &bh, &q0);
+    block_coords(BH, nq, BQ2, &bh, &q0);
     const int64_t hoff = (int64_t)bh * S * D;
     const uint16_t* Qh = Q + hoff;
     const uint16_t* Kh = K + hoff;
     const uint16_t* Vh = V + hoff;
 
-    // this lane's query row and its Q fragments (B operand of S^T = K Q^T)
+    // this lane's query row and its Q fragments (B operand of S^T = K Q^T).
+    // Loaded by asm so the compiler does not track them: it cannot count the
+    // copies issued after them (it loses track across the asm waits) and would
+    // drain every copy (vmcnt(0)) before the first use.  They are issued
+    // before the first copy, so the wait for tile 0 covers them.
     const int qw0 = q0 + wave * 32;
     const int qrow = qw0 + col;
-    bf16x8_t qf[D / 16];
+    u32x4_t qv[C::KS];
+    bf16x8_t qf[C::KS];  // set once Q has landed
     {
         const int qr = min(qrow, S - 1);  // rows past S compute on a valid row, never stored
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
-            qf[ks] = __builtin_bit_cast(
-                bf16x8_t, *reinterpret_cast<const u32x4_t*>(Qh + (int64_t)qr * D + ks * 16 + 8 * g));
+        for (int ks = 0; ks < C::KS; ++ks)
+            qv[ks] = global_b128_untracked(Qh + (int64_t)qr * D + ks * 16 + 8 * g);
     }
 
-    const int kv_end = CAUSAL ? min(S, q0 + BQ) : S;
-    const int n_kv = (kv_end + BKV - 1) / BKV;
+    const int kv_end = CAUSAL ? min(S, q0 + BQ2) : S;
+    const int n_kv = (kv_end + BKV - 1) / BKV;  // >= 1
 
-    // ---- LDS DMA of one K + V tile: wave w moves segments w, w+4, ... ----
-    constexpr int RPS = 1024 / C::ROW;  // rows per 1 KiB segment
-    auto dma = [&](uint8_t* Ks, uint8_t* Vs, int k0) {
+    // ---- copy piece p of tile t: p < SEGW a K segment, else a V segment;
+    // wave w moves segments w, w+8, ... of each operand tile ----
+    const uint32_t sm0 = (uint32_t)(uintptr_t)sm;
+    auto dma_tile = [&](int t) {
 #pragma unroll
-        for (int i = 0; i < C::NSEG / NW; ++i) {
-            const int seg = i * NW + wave;
-            const int r = seg * RPS + lane / C::UNITS;  // row within the tile
-            const int up = lane % C::UNITS;             // physical 16-byte unit
-            const int64_t key = min(k0 + r, S - 1);     // rows past S read a valid row
-            const int ku = up ^ (r & 7);
-            const int vu = up ^ (2 * (r & 3));
-            __builtin_amdgcn_global_load_lds(Kh + key * D + 8 * ku, (lds_void*)(Ks + seg * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(Vh + key * D + 8 * vu, (lds_void*)(Vs + seg * 1024), 16, 0, 0);
+        for (int p = 0; p < PIECES; ++p) {
+            const int i = p % C::SEGW;
+            const int seg = i * NW2 + wave;
+            const int r = seg * C::RPS + lane / C::UNITS;  // row within the tile
+            const int up = lane % C::UNITS;                // physical 16-byte unit
+            const int64_t key = min(t * BKV + r, S - 1);   // rows past S read a valid row
+            uint8_t* dst = sm + (t % C::NSTAGE) * C::STAGE + seg * 1024;
+            if (p < C::SEGW)
+                __builtin_amdgcn_global_load_lds(Kh + key * D + 8 * (up ^ kswz<D>(r)),
+                                                 (lds_void*)dst, 16, 0, 0);
+            else
+                __builtin_amdgcn_global_load_lds(Vh + key * D + 8 * (up ^ (vswz<D>(r) >> 1)),
+                                                 (lds_void*)(dst + C::TILE), 16, 0, 0);
         }
     };
 
-    f32x16_t acc_o[D / 32];
+    // ---- per-lane LDS offsets within a stage (recomputed per phase, which
+    // costs a few VALU ops in the MFMA phase but no registers across phases) ----
+    // K read for S MFMA i = (ks, half): key row half*32 + col, 16-byte unit 2 ks + g
+    auto k_off = [&](int ks) -> uint32_t {
+        return col * C::ROW + (((2 * ks + g) ^ kswz<D>(col)) << 4);
+    };
+    // V reads for PV MFMA (kk, dt): rows 16 kk + 4 g + s/4 (+8), chunk 8 dt + 4 vdh + s%4;
+    // the swizzle only depends on s/4, so (kk, half) is a constant row offset
+    auto v_off = [&](int dt) -> uint32_t {
+        const int vs = lane & 15, vdh = (lane >> 4) & 1;
+        const int r0 = 4 * g + (vs >> 2);
+        return C::TILE + r0 * C::ROW + (((8 * dt + 4 * vdh + (vs & 3)) ^ vswz<D>(r0)) << 3);
+    };
+
+    f32x16_t acc_o[C::DT];
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i)
+    for (int i = 0; i < C::DT; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc_o[i][e] = 0.0f;
+    f32x16_t sc[2];         // S_j: keys [32 h + 8 (e/4) + 4 g + e%4] of this lane's query
+    bf16x8_t pf[4];         // P_{j}: B operand of the PV product, 16-key step kk
     float m_run = kNegInf;  // running max of scaled scores, log2 domain
-    float l_run = 0.0f;     // this lane's partial running sum (its 16 keys per tile)
+    float l_run = 0.0f;     // this lane's partial running sum (its 32 keys per tile)
 
-    auto compute = [&](const uint8_t* Ks, const uint8_t* Vs, int k0) {
-        if (CAUSAL && k0 > qw0 + 31) return;  // whole tile above this wave's diagonal
-        f32x16_t s[BKV / 32];
+    // ---- MFMA(j): S_j (j < n_kv) and PV_{j-1} (j >= 1) ----
+    // The MFMA sequence alternates S and PV products when both are present:
+    // six independent accumulators in rotation, so no MFMA waits on the
+    // result of the one before it.  The LDS reads follow the same order (one
+    // K read per S MFMA, two V reads per PV MFMA) and are issued LA MFMAs
+    // ahead of their consumer.
+    auto mfma_phase = [&](int j, auto do_s_tag, auto do_pv_tag) {
+        constexpr bool DO_S = decltype(do_s_tag)::value;
+        constexpr bool DO_PV = decltype(do_pv_tag)::value;
+        using Q_ = MfmaSeq<DO_S, DO_PV, C::NS, C::NPV>;
+        constexpr int NM = Q_::NM;
+        constexpr int TOT = Q_::reads_upto(NM - 1);
+        const uint32_t kbase = sm0 + (j % C::NSTAGE) * C::STAGE;
+        const uint32_t vbase = sm0 + ((j + C::NSTAGE - 1) % C::NSTAGE) * C::STAGE;
+        uint32_t ka[C::KS], va[C::DT];
 #pragma unroll
-        for (int mt = 0; mt < BKV / 32; ++mt)
+        for (int ks = 0; ks < C::KS; ++ks) ka[ks] = kbase + k_off(ks);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[mt][e] = 0.0f;
-        // all K fragments of the tile first, so LDS latency hides under MFMAs
-        bf16x8_t kf[D / 16][BKV / 32];
+        for (int dt = 0; dt < C::DT; ++dt) va[dt] = vbase + v_off(dt);
+        u32x4_t kf[KR];
+        u32x2_t vlo[VR], vhi[VR];
+        // read r of the stream, r in MFMA order
+        auto issue_read = [&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            if constexpr (r < TOT) {
+                // the MFMA m this read belongs to, and which of its reads it is
+                constexpr int m = Q_::owner(r);
+                constexpr int first = m == 0 ? 0 : Q_::reads_upto(m - 1);
+                constexpr int i = Q_::idx(m);
+                if constexpr (Q_::is_s(m)) {
+                    constexpr int ks = i / 2, half = i % 2;
+                    kf[i % KR] = lds_b128<half * 32 * C::ROW>(ka[ks]);
+                } else {
+                    constexpr int kk = i / C::DT, dt = i % C::DT;
+                    if constexpr (r == first) vlo[i % VR] = lds_tr16<16 * kk * C::ROW>(va[dt]);
+                    else vhi[i % VR] = lds_tr16<(16 * kk + 8) * C::ROW>(va[dt]);
+                }
+            }
+        };
+        constexpr int R0 = Q_::reads_upto(LA - 1 < NM - 1 ? LA - 1 : NM - 1);
+        static_for<0, R0>(issue_read);
+        static_for<0, NM>([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            constexpr int i = Q_::idx(m);
+            constexpr int issued = Q_::reads_upto(m + LA - 1 < NM - 1 ? m + LA - 1 : NM - 1);
+            constexpr int need = Q_::reads_upto(m);
+            if constexpr (Q_::is_s(m)) {
+                lgkm_wait<issued - need>(kf[i % KR]);
+                // the first k-step starts from zero (an inline constant operand)
+                const f32x16_t zero = {};
+                sc[i % 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8_t, kf[i % KR]), qf[i / 2], i < 2 ? zero : sc[i % 2],
+                    0, 0, 0);
+            } else {
+                constexpr int kk = i / C::DT, dt = i % C::DT;
+                lgkm_wait2<issued - need>(vlo[i % VR], vhi[i % VR]);
+                const u32x2_t lo = vlo[i % VR], hi = vhi[i % VR];
+                const u32x4_t v4 = {lo[0], lo[1], hi[0], hi[1]};
+                acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8_t, v4), pf[kk], acc_o[dt], 0, 0, 0);
+            }
+            // keep LA MFMAs' reads in flight
+            constexpr int nxt = Q_::reads_upto(m + LA < NM - 1 ? m + LA : NM - 1);
+            static_for<issued, nxt>(issue_read);
+        });
+    };
+
+    // ---- SOFTMAX(j) ----
+    auto softmax_phase = [&](int j) {
+        const int k0 = j * BKV;
+        if (k0 + BKV > S || (CAUSAL && k0 + BKV - 1 > qw0)) {
+            // keys past S and (causal) keys after this lane's query -> -inf
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-            for (int mt = 0; mt < BKV / 32; ++mt)
-                kf[ks][mt] = *reinterpret_cast<const bf16x8_t*>(
-                    Ks + k_off(mt * 32 + col, 2 * ks + g, C::ROW));
-#pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks)
-#pragma unroll
-            for (int mt = 0; mt < BKV / 32; ++mt)
-                s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks][mt], qf[ks], s[mt], 0, 0, 0);
-        // masks: keys past S, and (causal) keys after this lane's query
-        const bool need_mask = (k0 + BKV > S) || (CAUSAL && k0 + BKV - 1 > qw0);
-        if (need_mask) {
-#pragma unroll
-            for (int mt = 0; mt < BKV / 32; ++mt)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const int key = k0 + mt * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-                    if (key >= S || (CAUSAL && key > qrow)) s[mt][e] = kNegInf;
+                    const int key = k0 + h * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+                    if (key >= S || (CAUSAL && key > qrow)) sc[h][e] = kNegInf;
                 }
         }
         float mx = kNegInf;
 #pragma unroll
-        for (int mt = 0; mt < BKV / 32; ++mt)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][e]);
-        mx = fmaxf(mx, xor32(mx)) * c_log2;
-        // lazy rescale: move the running max only when it grows by > kLazy
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[h][e]);
+        mx = pair_max(mx) * c_log2;
         const bool grow = mx > m_run + kLazy;
-        if (__ballot(grow)) {
-            const float m_new = grow ? mx : m_run;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
-            m_run = m_new;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;  // 0 on the first tile
+            m_run = grow ? mx : m_run;
             l_run *= alpha;
 #pragma unroll
-            for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+            for (int i = 0; i < C::DT; ++i) acc_o[i] *= alpha;
         }
         const float m_use = (m_run == kNegInf) ? 0.0f : m_run;  // row with no visible key yet
-        float ls = 0.0f;
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mt = 0; mt < BKV / 32; ++mt)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][e], c_log2, -m_use));
-                s[mt][e] = p;
-                ls += p;
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h][e], c_log2, -m_use));
+                sc[h][e] = p;
+                ls[e & 3] += p;
             }
-        l_run += ls;
-        // O^T += V^T P^T
-        const int vs = lane & 15, vdh = (lane >> 4) & 1;
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        asm volatile("" : "+v"(l_run));  // computed in this phase, not sunk into the next
 #pragma unroll
-        for (int kk = 0; kk < BKV / 16; ++kk) {
-            float pv[8];
+        for (int kk = 0; kk < 4; ++kk) {
+            u32x4_t u;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pv[e] = s[kk >> 1][8 * (kk & 1) + e];
-            const bf16x8_t pf = pack8(pv);
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const int c8 = 8 * dt + 4 * vdh + (vs & 3);
-                const int r0 = 16 * kk + 4 * g + (vs >> 2);
-                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s16x4*)(Vs + v_off(r0, c8, C::ROW)));
-                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s16x4*)(Vs + v_off(r0 + 8, c8, C::ROW)));
-                const s16x4_t v8[2] = {lo, hi};
-                const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, v8);
-                acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[dt], 0, 0, 0);
-            }
+            for (int w = 0; w < 4; ++w)
+                u[w] = pack_bf16x2(sc[kk >> 1][8 * (kk & 1) + 2 * w], sc[kk >> 1][8 * (kk & 1) + 2 * w + 1]);
+            reg_fence(u);
+            pf[kk] = __builtin_bit_cast(bf16x8_t, u);
         }
     };
 
-    if (n_kv > 0) {
-        dma(k_s0, v_s0, 0);
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA writes have landed
-        __syncthreads();
-        for (int j = 0; j < n_kv; j += 2) {
-            if (j + 1 < n_kv) dma(k_s1, v_s1, (j + 1) * BKV);
-            compute(k_s0, v_s0, j * BKV);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (j + 1 >= n_kv) break;
-            if (j + 2 < n_kv) dma(k_s0, v_s0, (j + 2) * BKV);
-            compute(k_s1, v_s1, (j + 1) * BKV);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+    // ---- prologue: Q, tiles 0 and 1 in flight; wait for Q and tile 0 ----
+    dma_tile(0);
+    if (n_kv > 1) dma_tile(1);
+    vm_wait(n_kv > 1 ? PIECES : 0);
+    bare_barrier();
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+        reg_fence(qv[ks]);  // after the wait above
+        qf[ks] = __builtin_bit_cast(bf16x8_t, qv[ks]);
+    }
+
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    // Phases 0 .. 2 n_kv + 1, each closed by a barrier of all 8 waves.
+    // Copies of tile u+2 are issued in phase 2u (into the stage tile u-2 left,
+    // last read in phase 2u-1).  Before phase 2u, tile u must have landed:
+    // the copies issued after it are those of tile u+1.
+    auto copy_ahead = [&](int u) {
+        if (u + 2 < n_kv) dma_tile(u + 2);
+    };
+    auto land = [&](int u) {
+        if (u < n_kv) vm_wait(u + 1 < n_kv ? PIECES : 0);
+    };
+    if (grp == 0) {
+        copy_ahead(0);
+        mfma_phase(0, yes{}, no{});
+        bare_barrier();  // phase 0
+        softmax_phase(0);
+        land(1);
+        bare_barrier();  // phase 1
+        for (int j = 1; j < n_kv; ++j) {
+            copy_ahead(j);
+            mfma_phase(j, yes{}, yes{});
+            bare_barrier();  // phase 2j
+            softmax_phase(j);
+            land(j + 1);
+            bare_barrier();  // phase 2j+1
         }
+        mfma_phase(n_kv, no{}, yes{});
+        bare_barrier();  // phase 2 n_kv
+        bare_barrier();  // phase 2 n_kv + 1
+    } else {
+        copy_ahead(0);
+        bare_barrier();  // phase 0
+        mfma_phase(0, yes{}, no{});
+        land(1);
+        bare_barrier();  // phase 1
+        for (int j = 1; j < n_kv; ++j) {
+            copy_ahead(j);
+            softmax_phase(j - 1);
+            bare_barrier();  // phase 2j
+            mfma_phase(j, yes{}, yes{});
+            land(j + 1);
+            bare_barrier();  // phase 2j+1
+        }
+        softmax_phase(n_kv - 1);
+        bare_barrier();  // phase 2 n_kv
+        mfma_phase(n_kv, no{}, yes{});
+        bare_barrier();  // phase 2 n_kv + 1
     }
 
     // ---- epilogue: O = acc / l, bf16; lse = (m + log2 l) * ln 2 ----
-    const float l_tot = l_run + xor32(l_run);
+    const float l_tot = pair_sum(l_run);
     const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
     if (qrow < S) {
         uint16_t* Orow = O + hoff + (int64_t)qrow * D;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
                 u32x2_t w;
@@ -300,6 +524,16 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_bf16(
         if (lse && g == 0)
             lse[(int64_t)bh * S + qrow] = (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f;
     }
+}
+
+// The body lives in a device function: with it inline in the kernel template,
+// clang's host pass silently skipped the kernel's launch stub.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void flash_fwd_bf16(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ lse, int BH, int S,
+    float c_log2) {
+    flash_bf16_body<D, CAUSAL>(Q, K, V, O, lse, BH, S, c_log2);
 }
 
 // ---------------------------------------------------------------------------
@@ -330,7 +564,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_f32(
     const int g = lane >> 5, col = lane & 31;
     const int nq = (S + BQ - 1) / BQ;
     int bh, q0;
-    block_coords(BH, nq, &bh, &q0);
+    block_coords(BH, nq, BQ, &bh, &q0);
     const int64_t hoff = (int64_t)bh * S * D;
     const float* Qh = Q + hoff;
     const float* Kh = K + hoff;
@@ -465,8 +699,11 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_f32(
 template <typename KFN, typename T>
 hipError_t go(KFN kfn, const void* Q, const void* K, const void* V, void* O, float* lse, int BH,
               int S, float c_log2, hipStream_t s) {
-    const int nq = (S + BQ - 1) / BQ;
-    hipLaunchKernelGGL(kfn, dim3(BH * nq), dim3(NW * 64), 0, s, static_cast<const T*>(Q),
+    // bf16: 256-row blocks of 8 waves; fp32: 128-row blocks of 4 waves
+    constexpr bool BF = sizeof(T) == 2;
+    const int bq = BF ? BQ2 : BQ;
+    const int nq = (S + bq - 1) / bq;
+    hipLaunchKernelGGL(kfn, dim3(BH * nq), dim3((BF ? NW2 : NW) * 64), 0, s, static_cast<const T*>(Q),
                        static_cast<const T*>(K), static_cast<const T*>(V), static_cast<T*>(O), lse,
                        BH, S, c_log2);
     return hipGetLastError();
