@@ -20,7 +20,7 @@
 //
 // Work split: a workgroup (8 waves) owns 256 columns and one of KS K-ranges;
 // every wave takes its own 32-row k-steps of that range, issuing all of its
-// weight loads for up to 4 k-steps before converting the first.  The 8 wave
+// weight loads for 2 k-steps before converting the first.  The 8 wave
 // partials are summed in LDS in a fixed tree order and the workgroup stores
 // its fp32 partial tile to the workspace.  A second, small kernel sums the KS
 // partials of every output in split order and applies scale, bias and the
@@ -38,7 +38,7 @@ constexpr int COLS = 256;       // columns per workgroup: 16 lanes x 16 columns
 constexpr int WAVES = 8;
 constexpr int THREADS = WAVES * 64;
 constexpr int KSTEP = 32;       // rows per MFMA k-step
-constexpr int GROUP = 4;        // k-steps whose loads are in flight together
+constexpr int GROUP = 2;        // k-steps whose loads are in flight together
 
 struct Plan {
     int ks;         // number of K splits (partials)
@@ -47,8 +47,10 @@ struct Plan {
 
 inline Plan plan(int K) {
     const int total_steps = (K + KSTEP - 1) / KSTEP;
-    // aim for GROUP k-steps per wave; at most 16 splits
-    int ks = (total_steps + WAVES * GROUP - 1) / (WAVES * GROUP);
+    // aim for two groups of GROUP k-steps per wave (measured best at
+    // K = N = 8192: fewer splits starve the chip, more cost partial traffic);
+    // at most 16 splits
+    int ks = (total_steps + 2 * WAVES * GROUP - 1) / (2 * WAVES * GROUP);
     if (ks > 16) ks = 16;
     if (ks < 1) ks = 1;
     const int per_split = (total_steps + ks - 1) / ks;
