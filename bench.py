@@ -32,9 +32,9 @@ PEAK = {"bf16": 2516.6, "f32": 157.3, "hbm": 8000.0}  # TFLOP/s, TFLOP/s, GB/s
 # counters read for a 64 MiB device copy (fetch x2.0, write x1.0).  They are
 # re-measured whenever a kernel changes; None where not measured.
 MEASURED_TRAFFIC = {
-    "c3": 202.1e6 + 34.5e6,   # gemm_bf16_kernel<GELU>
-    "c4": 809.0e6 + 268.4e6,  # flash_fwd_bf16<128, causal>
-    "c5": 68.4e6 + 2.1e6 + 2.2e6 + 0.1e6,  # w8a16 partial + finalize
+    "c3": 201.7e6 + 33.9e6,   # gemm_bf16_dma_kernel<GELU>
+    "c4": 806.1e6 + 268.4e6,  # flash_fwd_bf16<128, causal>
+    "c5": 68.3e6 + 2.1e6 + 2.2e6 + 0.1e6,  # w8a16 partial + finalize
 }
 
 
@@ -303,7 +303,7 @@ def main():
     r = step[dom]
     roofline = {"bound": r.bound, "achieved": r.rate(avg[dom]), "peak": r.peak, "unit": r.unit,
                 "frac": r.rate(avg[dom]) / r.peak, "traffic": MEASURED_TRAFFIC.get(r.name),
-                "kernel": {"c3": "gemm_bf16_kernel<GELU>", "c4": "flash_fwd_bf16"}[r.name],
+                "kernel": {"c3": "gemm_bf16_dma_kernel<GELU>", "c4": "flash_fwd_bf16"}[r.name],
                 "avg_launch_ms": avg[dom]}
     step_kernels = {x.name: {"avg_ms": a, "achieved": x.rate(a), "frac": x.rate(a) / x.peak}
                     for x, a in zip(step, avg)}
