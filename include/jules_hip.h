@@ -164,10 +164,50 @@ int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M,
                           int N, int K, float scale_A, float scale_B,
                           const float* bias, void* stream);
 
+/* ---- row kernels ----------------------------------------------------------
+ * fp32, row-major [M, N], device pointers, 4-byte aligned; out may alias in.
+ * Each row is processed with the reference's per-element arithmetic (exp
+ * split: fast_exp for j < N & ~15, expf for the tail; reciprocal multiply
+ * vs divide likewise); sums are taken in a fixed tree order, so results
+ * match the reference to rounding and are deterministic run to run.
+ *
+ * jules_hip_softmax: out[i,:] = softmax(in[i,:]).
+ *   Replaces fusedSoftmax(output, input, M, N)
+ *   (reference include/jules/Kernel/FusedKernels.h:464-526); routed name
+ *   "fusedSoftmax" (KernelRoutingPass.cpp:261).
+ *
+ * jules_hip_layernorm: out[i,j] = (in[i,j]-mean_i)*rstd_i*gamma[j] + beta[j],
+ *   rstd_i = 1/sqrtf(var_i + epsilon), population variance.
+ *   Replaces fusedLayerNorm(output, input, gamma, beta, M, N, epsilon)
+ *   (FusedKernels.h:532-600; the reference's default epsilon is 1e-5f);
+ *   routed name "fusedLayerNorm" (KernelRoutingPass.cpp:330).
+ *
+ * jules_hip_cross_entropy: grad[i,:] = (softmax(logits[i,:]) - onehot(t_i))/M,
+ *   *loss = mean_i -logf(p_i[t_i] + 1e-10f), written to device memory.
+ *   Replaces float fusedCrossEntropyLoss(logits, targets, grad, M, N)
+ *   (FusedKernels.h:766-854), which returns the loss by value; routed name
+ *   "fusedCrossEntropyLoss" (KernelRoutingPass.cpp:378).  targets: int32 [M]
+ *   on the device; a target outside [0, N) gives a NaN loss for its row
+ *   (the reference reads out of bounds).  workspace: device memory of at
+ *   least jules_hip_cross_entropy_workspace_size(M) bytes (per-row losses),
+ *   overwritten by every call; M = 0 writes a NaN loss (0/0, as the
+ *   reference's total_loss / M).
+ */
+int jules_hip_softmax(float* out, const float* in, int M, int N, void* stream);
+int jules_hip_layernorm(float* out, const float* in, const float* gamma,
+                        const float* beta, int M, int N, float epsilon,
+                        void* stream);
+size_t jules_hip_cross_entropy_workspace_size(int M);
+int jules_hip_cross_entropy(const float* logits, const int32_t* targets,
+                            float* grad, float* loss, int M, int N,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* ---- kernel-name registry -------------------------------------------------
  * Resolves the names KernelRoutingPass emits (fusedMatmul{Relu,Sigmoid,Tanh,
  * Gelu}, fusedMatmulBias{Relu,Sigmoid,Tanh,Gelu}, fusedGelu, matmulInt8,
- * flashAttention) and the ones this library adds (fusedMatmul,
+ * flashAttention, fusedSoftmax, fusedLayerNorm, fusedCrossEntropyLoss) and
+ * the ones this library adds (fusedMatmul,
  * fusedMatmulBias, fusedMatmulBiasSilu, flashAttentionCausal,
  * matmulW8A16BiasSilu) to a descriptor-based entry point.  The descriptor
  * extends the reference's TensorDescriptor (include/jules/LLVMBackend.h:60-66:
@@ -178,8 +218,12 @@ int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M,
  * (x, W, scale[, bias]) for W8A16, (A, B[, bias]) plus backend_config
  * "scale_a=<f>,scale_b=<f>" for matmulInt8 (the reference emits no scales,
  * KernelRoutingPass.cpp:406-410).  Attention accepts backend_config
- * "scale=<f>"; the default is 1/sqrtf(D).  W8A16 needs a workspace; its
- * registry entry allocates one per device on first use.
+ * "scale=<f>"; the default is 1/sqrtf(D).  Row kernels: (x) -> y for
+ * fusedSoftmax, (x, gamma, beta) -> y with backend_config "epsilon=<f>"
+ * (default 1e-5) for fusedLayerNorm, (logits, targets) -> (grad, loss) for
+ * fusedCrossEntropyLoss (loss: one fp32 element); rows are the last
+ * dimension.  W8A16 and cross entropy need a workspace; their registry
+ * entries allocate one per device on first use.
  */
 typedef struct jh_tensor {
     void* data;

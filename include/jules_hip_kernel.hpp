@@ -104,6 +104,13 @@ void tiledMatmulWithActivation(const float* A, const float* B, float* C, int M, 
                                const TileConfig& cfg, ActivationType act = ActivationType::None);
 // reference FusedKernels.h:606
 void fusedGelu(float* output, const float* input, int N);
+// reference FusedKernels.h:464
+void fusedSoftmax(float* output, const float* input, int M, int N);
+// reference FusedKernels.h:532
+void fusedLayerNorm(float* output, const float* input, const float* gamma, const float* beta,
+                    int M, int N, float epsilon = 1e-5f);
+// reference FusedKernels.h:766; returns the mean loss (NaN on failure)
+float fusedCrossEntropyLoss(const float* logits, const int32_t* targets, float* grad, int M, int N);
 // reference FusedKernels.h:867 (scalar-path semantics)
 void matmulInt8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K, float scale_A,
                 float scale_B, const float* bias = nullptr, ExecutionArena* arena = nullptr);

@@ -7,7 +7,9 @@
 // nothing and abort() on arena overflow, ExecutionArena.h:140-143).
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
+#include <cstdint>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -170,6 +172,62 @@ int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int
                      "matmulInt8 launch");
 }
 
+// Row kernels (reference FusedKernels.h:464-526, :532-600, :766-854).
+static int row_shape(const char* who, int M, int N) {
+    if (M < 0 || N < 0) return fail(JH_ERR_SHAPE, "%s: M=%d N=%d", who, M, N);
+    if ((int64_t)M * N > kMaxElems) return fail(JH_ERR_SHAPE, "%s: M=%d N=%d too large", who, M, N);
+    return JH_OK;
+}
+
+int jules_hip_softmax(float* out, const float* in, int M, int N, void* stream) {
+    int st = row_shape("softmax", M, N);
+    if (st != JH_OK) return st;
+    if (M == 0 || N == 0) return JH_OK;
+    if (!out || !in) return fail(JH_ERR_NULL, "softmax: null pointer");
+    if (!aligned(out, 4) || !aligned(in, 4)) return fail(JH_ERR_ALIGN, "softmax: alignment");
+    return check_hip(jh::launch_softmax(out, in, M, N, static_cast<hipStream_t>(stream)),
+                     "softmax launch");
+}
+
+int jules_hip_layernorm(float* out, const float* in, const float* gamma, const float* beta,
+                        int M, int N, float epsilon, void* stream) {
+    int st = row_shape("layernorm", M, N);
+    if (st != JH_OK) return st;
+    if (!(std::isfinite(epsilon) && epsilon >= 0.0f))
+        return fail(JH_ERR_ARG, "layernorm: epsilon %g", epsilon);
+    if (M == 0 || N == 0) return JH_OK;
+    if (!out || !in || !gamma || !beta) return fail(JH_ERR_NULL, "layernorm: null pointer");
+    if (!aligned(out, 4) || !aligned(in, 4) || !aligned(gamma, 4) || !aligned(beta, 4))
+        return fail(JH_ERR_ALIGN, "layernorm: alignment");
+    return check_hip(jh::launch_layernorm(out, in, gamma, beta, M, N, epsilon,
+                                          static_cast<hipStream_t>(stream)),
+                     "layernorm launch");
+}
+
+size_t jules_hip_cross_entropy_workspace_size(int M) {
+    return M > 0 ? (size_t)M * sizeof(float) : sizeof(float);
+}
+
+int jules_hip_cross_entropy(const float* logits, const int32_t* targets, float* grad, float* loss,
+                            int M, int N, void* workspace, size_t workspace_bytes, void* stream) {
+    int st = row_shape("cross_entropy", M, N);
+    if (st != JH_OK) return st;
+    if (M > 0 && N == 0) return fail(JH_ERR_SHAPE, "cross_entropy: N=0 with M=%d rows", M);
+    if (!loss) return fail(JH_ERR_NULL, "cross_entropy: null loss");
+    if (M > 0 && (!logits || !targets || !grad))
+        return fail(JH_ERR_NULL, "cross_entropy: null logits, targets or grad");
+    if (!workspace || workspace_bytes < jules_hip_cross_entropy_workspace_size(M))
+        return fail(JH_ERR_WORKSPACE, "cross_entropy: workspace needs %zu bytes",
+                    jules_hip_cross_entropy_workspace_size(M));
+    if (!aligned(logits, 4) || !aligned(targets, 4) || !aligned(grad, 4) || !aligned(loss, 4) ||
+        !aligned(workspace, 4))
+        return fail(JH_ERR_ALIGN, "cross_entropy: alignment");
+    return check_hip(jh::launch_cross_entropy(logits, targets, grad, loss,
+                                              static_cast<float*>(workspace), M, N,
+                                              static_cast<hipStream_t>(stream)),
+                     "cross_entropy launch");
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
@@ -296,8 +354,8 @@ int k_attn_causal(int ni, const jh_tensor* in, int no, jh_tensor* out, const cha
     return attention_desc(1, ni, in, no, out, c, s);
 }
 
-// One W8A16 workspace per device, grown on demand, for callers of the
-// registry who cannot pass one.  Guarded by a mutex; calls that share a
+// One workspace per device (W8A16 partials, cross-entropy row losses), grown
+// on demand, for callers of the registry who cannot pass one.  Guarded by a mutex; calls that share a
 // device through this path are serialised by the caller's stream order.
 std::mutex g_ws_mu;
 void* g_ws[64];
@@ -306,15 +364,15 @@ size_t g_ws_bytes[64];
 int registry_workspace(size_t need, void** ws) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-        return fail(JH_ERR_HIP, "w8a16 registry: hipGetDevice");
+        return fail(JH_ERR_HIP, "registry workspace: hipGetDevice");
     std::lock_guard<std::mutex> lock(g_ws_mu);
     if (g_ws_bytes[dev] < need) {
         if (g_ws[dev]) (void)hipFree(g_ws[dev]);
         g_ws[dev] = nullptr;
         g_ws_bytes[dev] = 0;
         void* p = nullptr;
-        if (hipMalloc(&p, need) != hipSuccess) return fail(JH_ERR_HIP, "w8a16 registry: hipMalloc");
-        if (hipMemset(p, 0, need) != hipSuccess) return fail(JH_ERR_HIP, "w8a16 registry: hipMemset");
+        if (hipMalloc(&p, need) != hipSuccess) return fail(JH_ERR_HIP, "registry workspace: hipMalloc");
+        if (hipMemset(p, 0, need) != hipSuccess) return fail(JH_ERR_HIP, "registry workspace: hipMemset");
         g_ws[dev] = p;
         g_ws_bytes[dev] = need;
     }
@@ -380,14 +438,78 @@ int k_int8(int ni, const jh_tensor* in, int no, jh_tensor* out, const char* cfg,
                                  bias, s);
 }
 
+// rows of a descriptor: product of all but the last dimension
+int64_t rows_of(const jh_tensor& t) {
+    int64_t r = 1;
+    for (int d = 0; d + 1 < t.rank; ++d) r *= t.sizes[d];
+    return r;
+}
+
+int k_softmax(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
+    if (ni != 1 || no != 1 || !in || !out) return fail(JH_ERR_ARG, "fusedSoftmax: (x) -> y");
+    const jh_tensor& x = in[0];
+    jh_tensor& y = out[0];
+    if (x.rank < 1 || !contiguous(x) || !contiguous(y) || numel(x) != numel(y) ||
+        y.sizes[y.rank - 1] != x.sizes[x.rank - 1])
+        return fail(JH_ERR_SHAPE, "fusedSoftmax: contiguous x and y of one shape");
+    if (x.dtype != JH_F32 || y.dtype != JH_F32) return fail(JH_ERR_DTYPE, "fusedSoftmax: fp32");
+    const int64_t N = x.sizes[x.rank - 1], M = rows_of(x);
+    if (M > INT32_MAX || N > INT32_MAX) return fail(JH_ERR_SHAPE, "fusedSoftmax: too large");
+    return jules_hip_softmax(static_cast<float*>(addr_mut(y)), static_cast<const float*>(addr(x)),
+                             (int)M, (int)N, s);
+}
+
+int k_layernorm(int ni, const jh_tensor* in, int no, jh_tensor* out, const char* cfg, void* s) {
+    if (ni != 3 || no != 1 || !in || !out)
+        return fail(JH_ERR_ARG, "fusedLayerNorm: (x, gamma, beta) -> y");
+    const jh_tensor &x = in[0], &g = in[1], &b = in[2];
+    jh_tensor& y = out[0];
+    if (x.rank < 1 || !contiguous(x) || !contiguous(y) || !contiguous(g) || !contiguous(b) ||
+        numel(x) != numel(y))
+        return fail(JH_ERR_SHAPE, "fusedLayerNorm: contiguous operands");
+    const int64_t N = x.sizes[x.rank - 1], M = rows_of(x);
+    if (numel(g) != N || numel(b) != N) return fail(JH_ERR_SHAPE, "fusedLayerNorm: gamma/beta [N]");
+    if (x.dtype != JH_F32 || y.dtype != JH_F32 || g.dtype != JH_F32 || b.dtype != JH_F32)
+        return fail(JH_ERR_DTYPE, "fusedLayerNorm: fp32");
+    if (M > INT32_MAX || N > INT32_MAX) return fail(JH_ERR_SHAPE, "fusedLayerNorm: too large");
+    float eps = 1e-5f;  // reference default, FusedKernels.h:534
+    config_float(cfg, "epsilon", &eps);
+    return jules_hip_layernorm(static_cast<float*>(addr_mut(y)), static_cast<const float*>(addr(x)),
+                               static_cast<const float*>(addr(g)),
+                               static_cast<const float*>(addr(b)), (int)M, (int)N, eps, s);
+}
+
+int k_cross_entropy(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
+    if (ni != 2 || no != 2 || !in || !out)
+        return fail(JH_ERR_ARG, "fusedCrossEntropyLoss: (logits, targets) -> (grad, loss)");
+    const jh_tensor &x = in[0], &t = in[1];
+    jh_tensor &g = out[0], &l = out[1];
+    if (x.rank < 1 || !contiguous(x) || !contiguous(t) || !contiguous(g) || !contiguous(l) ||
+        numel(g) != numel(x) || numel(l) != 1)
+        return fail(JH_ERR_SHAPE, "fusedCrossEntropyLoss: contiguous operands, one loss element");
+    const int64_t N = x.sizes[x.rank - 1], M = rows_of(x);
+    if (numel(t) != M) return fail(JH_ERR_SHAPE, "fusedCrossEntropyLoss: one target per row");
+    if (x.dtype != JH_F32 || g.dtype != JH_F32 || l.dtype != JH_F32 || t.dtype != JH_I32)
+        return fail(JH_ERR_DTYPE, "fusedCrossEntropyLoss: fp32 logits/grad/loss, int32 targets");
+    if (M > INT32_MAX || N > INT32_MAX) return fail(JH_ERR_SHAPE, "fusedCrossEntropyLoss: too large");
+    const size_t need = jules_hip_cross_entropy_workspace_size((int)M);
+    void* ws = nullptr;
+    const int st = registry_workspace(need, &ws);
+    if (st != JH_OK) return st;
+    return jules_hip_cross_entropy(static_cast<const float*>(addr(x)),
+                                   static_cast<const int32_t*>(addr(t)),
+                                   static_cast<float*>(addr_mut(g)),
+                                   static_cast<float*>(addr_mut(l)), (int)M, (int)N, ws, need, s);
+}
+
 struct Entry {
     const char* name;
     jh_kernel_fn fn;
 };
 
 // Names emitted by KernelRoutingPass (lib/Passes/KernelRoutingPass.cpp:144-166,
-// :189-211, :287, :409) and listed in KernelRoutingPass.h:13-23, then the
-// names this library adds.
+// :189-211, :261, :287, :330, :378, :409) and listed in KernelRoutingPass.h:13-23,
+// then the names this library adds.
 const Entry kRegistry[] = {
     {"fusedMatmulRelu", k_matmul_relu},
     {"fusedMatmulSigmoid", k_matmul_sigmoid},
@@ -399,6 +521,9 @@ const Entry kRegistry[] = {
     {"fusedGelu", k_gelu},
     {"matmulInt8", k_int8},
     {"flashAttention", k_attn},
+    {"fusedSoftmax", k_softmax},
+    {"fusedLayerNorm", k_layernorm},
+    {"fusedCrossEntropyLoss", k_cross_entropy},
     {"fusedMatmul", k_matmul},
     {"fusedMatmulBias", k_matmul_bias},
     {"fusedMatmulBiasGelu", k_matmul_bias_gelu},

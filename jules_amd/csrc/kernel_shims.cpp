@@ -3,9 +3,12 @@
 // and the call is synchronous, as the reference's CPU kernels are.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <string>
+#include <vector>
 
 #include "jules_hip.h"
 #include "jules_hip_kernel.hpp"
@@ -191,6 +194,61 @@ void fusedGelu(float* output, const float* input, int N) {
     if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
     if (st == JH_OK && !out.finish()) st = JH_ERR_HIP;
     record(st);
+}
+
+void fusedSoftmax(float* output, const float* input, int M, int N) {
+    if (M < 0 || N < 0) return record(JH_ERR_SHAPE);
+    const size_t bytes = sizeof(float) * (size_t)M * (size_t)N;
+    DevBuf in(input, bytes, true, false), out(output, bytes, false, true);
+    if (!in.ok() || !out.ok()) return record(JH_ERR_HIP);
+    int st = jules_hip_softmax(static_cast<float*>(out.get()), static_cast<const float*>(in.get()),
+                               M, N, nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !out.finish()) st = JH_ERR_HIP;
+    record(st);
+}
+
+void fusedLayerNorm(float* output, const float* input, const float* gamma, const float* beta,
+                    int M, int N, float epsilon) {
+    if (M < 0 || N < 0) return record(JH_ERR_SHAPE);
+    const size_t bytes = sizeof(float) * (size_t)M * (size_t)N;
+    const size_t nb = sizeof(float) * (size_t)N;
+    DevBuf in(input, bytes, true, false), out(output, bytes, false, true);
+    DevBuf g(gamma, nb, true, false), b(beta, nb, true, false);
+    if (!in.ok() || !out.ok() || !g.ok() || !b.ok()) return record(JH_ERR_HIP);
+    int st = jules_hip_layernorm(static_cast<float*>(out.get()), static_cast<const float*>(in.get()),
+                                 static_cast<const float*>(g.get()),
+                                 static_cast<const float*>(b.get()), M, N, epsilon, nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !out.finish()) st = JH_ERR_HIP;
+    record(st);
+}
+
+float fusedCrossEntropyLoss(const float* logits, const int32_t* targets, float* grad, int M,
+                            int N) {
+    const float nan = std::numeric_limits<float>::quiet_NaN();
+    if (M < 0 || N < 0) {
+        record(JH_ERR_SHAPE);
+        return nan;
+    }
+    const size_t bytes = sizeof(float) * (size_t)M * (size_t)N;
+    float loss = nan;
+    std::vector<float> ws_host(std::max<size_t>(1, (size_t)M));
+    DevBuf x(logits, bytes, true, false), t(targets, sizeof(int32_t) * (size_t)M, true, false);
+    DevBuf g(grad, bytes, false, true), l(&loss, sizeof(float), false, true);
+    DevBuf ws(ws_host.data(), sizeof(float) * ws_host.size(), false, false);
+    if (!x.ok() || !t.ok() || !g.ok() || !l.ok() || !ws.ok()) {
+        record(JH_ERR_HIP);
+        return nan;
+    }
+    int st = jules_hip_cross_entropy(static_cast<const float*>(x.get()),
+                                     static_cast<const int32_t*>(t.get()),
+                                     static_cast<float*>(g.get()), static_cast<float*>(l.get()), M,
+                                     N, ws.get(), sizeof(float) * ws_host.size(), nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && (!g.finish() || !l.finish())) st = JH_ERR_HIP;
+    record(st);
+    return st == JH_OK ? loss : nan;
 }
 
 void matmulInt8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K, float scale_A,

@@ -22,5 +22,11 @@ hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float
                         hipStream_t s);
 hipError_t launch_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                               float scale_a, float scale_b, const float* bias, hipStream_t s);
+hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t s);
+hipError_t launch_layernorm(float* out, const float* in, const float* gamma, const float* beta,
+                            int M, int N, float eps, hipStream_t s);
+// row_loss: M floats of scratch (per-row losses before the fixed-order sum)
+hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, float* grad,
+                                float* loss, float* row_loss, int M, int N, hipStream_t s);
 
 }  // namespace jh

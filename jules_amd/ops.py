@@ -140,3 +140,52 @@ def matmul_int8(A, B, scale_a, scale_b, bias=None, out=None):
     check(lib().jules_hip_matmul_int8(_ptr(A), _ptr(B), _ptr(out), M, N, K, float(scale_a),
                                       float(scale_b), _ptr(bias), _stream(A)))
     return out
+
+
+def _rows(x):
+    N = x.shape[-1] if x.dim() > 0 else 1
+    return x.numel() // max(N, 1) if N else 0, N
+
+
+def softmax(x, out=None):
+    """fusedSoftmax (FusedKernels.h:464) over the last dimension of fp32 x."""
+    _need(x, "x", (torch.float32,))
+    if out is None:
+        out = torch.empty_like(x)
+    M, N = _rows(x)
+    check(lib().jules_hip_softmax(_ptr(out), _ptr(x), M, N, _stream(x)))
+    return out
+
+
+def layernorm(x, gamma, beta, eps=1e-5, out=None):
+    """fusedLayerNorm (FusedKernels.h:532) over the last dimension of fp32 x."""
+    _need(x, "x", (torch.float32,))
+    _need(gamma, "gamma", (torch.float32,), x.device)
+    _need(beta, "beta", (torch.float32,), x.device)
+    if out is None:
+        out = torch.empty_like(x)
+    M, N = _rows(x)
+    check(lib().jules_hip_layernorm(_ptr(out), _ptr(x), _ptr(gamma), _ptr(beta), M, N,
+                                    float(eps), _stream(x)))
+    return out
+
+
+def cross_entropy_workspace(M, device):
+    nbytes = lib().jules_hip_cross_entropy_workspace_size(int(M))
+    return torch.empty(((nbytes + 3) // 4,), dtype=torch.float32, device=device)
+
+
+def cross_entropy(logits, targets, grad=None, loss=None, workspace=None):
+    """fusedCrossEntropyLoss (FusedKernels.h:766): returns (loss[1], grad) on the device."""
+    _need(logits, "logits", (torch.float32,))
+    _need(targets, "targets", (torch.int32,), logits.device)
+    M, N = _rows(logits)
+    if grad is None:
+        grad = torch.empty_like(logits)
+    if loss is None:
+        loss = torch.empty((1,), dtype=torch.float32, device=logits.device)
+    if workspace is None:
+        workspace = cross_entropy_workspace(M, logits.device)
+    check(lib().jules_hip_cross_entropy(_ptr(logits), _ptr(targets), _ptr(grad), _ptr(loss), M, N,
+                                        _ptr(workspace), workspace.numel() * 4, _stream(logits)))
+    return loss, grad

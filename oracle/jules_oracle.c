@@ -526,3 +526,164 @@ void jo_set_threads(int n) {
     (void)n;
 #endif
 }
+
+/* ======================================================================
+ * Row kernels.  The reference's AVX-512 path keeps 16 lane partials for
+ * the part of a row that fills whole 16-float vectors (j < N & ~15), folds
+ * them with _mm512_reduce_* and finishes the < 16 tail with scalar code
+ * (libm expf, sequential adds).  reduce16 folds the lanes by halves
+ * (8+8, 4+4, 2+2, 1+1), the order of the GCC reduce intrinsics; the tail
+ * is the reference's scalar loop.
+ * ====================================================================== */
+static float reduce16_add(const float* v) {
+    float a[8], b[4], c[2];
+    for (int i = 0; i < 8; ++i) a[i] = v[i + 8] + v[i];
+    for (int i = 0; i < 4; ++i) b[i] = a[i + 4] + a[i];
+    c[0] = b[0] + b[2];
+    c[1] = b[1] + b[3];
+    return c[0] + c[1];
+}
+static float reduce16_max(const float* v) {
+    float m = v[0];
+    for (int i = 1; i < 16; ++i) m = (v[i] > m) ? v[i] : m;
+    return m;
+}
+
+/* One softmax row into out (reference FusedKernels.h:467-509): returns the
+ * row sum.  The vector part uses fast_exp and out = e * (1/sum); the tail
+ * uses expf and out = e / sum. */
+static float softmax_row(float* out, const float* in, int N) {
+    const int nv = N & ~15;
+    float lane[16];
+    for (int l = 0; l < 16; ++l) lane[l] = -FLT_MAX;
+    /* _mm512_max_ps(acc, x) = acc > x ? acc : x (MAXPS returns its second
+     * operand on NaN); std::max(m, x) = m < x ? x : m */
+    for (int j = 0; j < nv; j += 16)
+        for (int l = 0; l < 16; ++l) lane[l] = (lane[l] > in[j + l]) ? lane[l] : in[j + l];
+    float mx = reduce16_max(lane); /* _mm512_reduce_max_ps */
+    for (int j = nv; j < N; ++j) mx = (mx < in[j]) ? in[j] : mx;
+    for (int l = 0; l < 16; ++l) lane[l] = 0.0f;
+    for (int j = 0; j < nv; j += 16)
+        for (int l = 0; l < 16; ++l) {
+            const float e = jo_fast_exp(in[j + l] - mx);
+            out[j + l] = e;
+            lane[l] = lane[l] + e;
+        }
+    float sum = reduce16_add(lane);
+    for (int j = nv; j < N; ++j) {
+        const float e = expf(in[j] - mx);
+        out[j] = e;
+        sum += e;
+    }
+    const float inv = 1.0f / sum;
+    for (int j = 0; j < nv; ++j) out[j] = out[j] * inv;
+    for (int j = nv; j < N; ++j) out[j] = out[j] / sum;
+    return sum;
+}
+
+/* fusedSoftmax, reference FusedKernels.h:464-526 (AVX-512 branch) */
+void jo_softmax(float* out, const float* in, int M, int N) {
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) softmax_row(out + (int64_t)i * N, in + (int64_t)i * N, N);
+}
+
+/* fusedLayerNorm, reference FusedKernels.h:532-600 (AVX-512 branch).
+ * Mean and variance: 16 lane partials over the vector part (the variance
+ * with _mm512_fmadd_ps), reduce, scalar tail, then / N.  The tail's
+ * `var += diff * diff` and `(x - mean) * inv_std * gamma + beta` are taken
+ * as contracted to fma, as GCC does for C++ when FMA is available (the
+ * vector path uses _mm512_fmadd_ps for both). */
+void jo_layernorm(float* out, const float* in, const float* gamma, const float* beta,
+                  int M, int N, float eps) {
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) {
+        const float* x = in + (int64_t)i * N;
+        float* y = out + (int64_t)i * N;
+        const int nv = N & ~15;
+        float lane[16];
+        for (int l = 0; l < 16; ++l) lane[l] = 0.0f;
+        for (int j = 0; j < nv; j += 16)
+            for (int l = 0; l < 16; ++l) lane[l] = lane[l] + x[j + l];
+        float mean = reduce16_add(lane);
+        for (int j = nv; j < N; ++j) mean += x[j];
+        mean /= (float)N;
+        for (int l = 0; l < 16; ++l) lane[l] = 0.0f;
+        for (int j = 0; j < nv; j += 16)
+            for (int l = 0; l < 16; ++l) {
+                const float d = x[j + l] - mean;
+                lane[l] = fmaf(d, d, lane[l]);
+            }
+        float var = reduce16_add(lane);
+        for (int j = nv; j < N; ++j) {
+            const float d = x[j] - mean;
+            var = fmaf(d, d, var);
+        }
+        var /= (float)N;
+        const float inv_std = 1.0f / sqrtf(var + eps);
+        for (int j = 0; j < N; ++j) y[j] = fmaf((x[j] - mean) * inv_std, gamma[j], beta[j]);
+    }
+}
+
+/* fusedCrossEntropyLoss, reference FusedKernels.h:766-854 (AVX-512 branch):
+ * grad = softmax(logits) - onehot(target), divided by M; returns the mean of
+ * -log(p[target] + 1e-10).  The reference sums the row losses with an
+ * OpenMP reduction (thread-dependent order); here they are summed in row
+ * order. */
+float jo_cross_entropy(const float* logits, const int32_t* targets, float* grad, int M, int N) {
+    float* row_loss = (float*)malloc(sizeof(float) * (size_t)(M > 0 ? M : 1));
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) {
+        float* g = grad + (int64_t)i * N;
+        softmax_row(g, logits + (int64_t)i * N, N);
+        const int t = targets[i];
+        row_loss[i] = -logf(g[t] + 1e-10f);
+        g[t] -= 1.0f;
+        for (int j = 0; j < N; ++j) g[j] /= (float)M;
+    }
+    float total = 0.0f;
+    for (int i = 0; i < M; ++i) total += row_loss[i];
+    free(row_loss);
+    return total / (float)M;
+}
+
+/* ---- fp64: textbook definitions ---- */
+void jo64_softmax(double* out, const float* in, int M, int N) {
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) {
+        const float* x = in + (int64_t)i * N;
+        double* y = out + (int64_t)i * N;
+        double mx = -INFINITY, s = 0.0;
+        for (int j = 0; j < N; ++j) mx = x[j] > mx ? x[j] : mx;
+        for (int j = 0; j < N; ++j) s += (y[j] = exp((double)x[j] - mx));
+        for (int j = 0; j < N; ++j) y[j] /= s;
+    }
+}
+
+void jo64_layernorm(double* out, const float* in, const float* gamma, const float* beta,
+                    int M, int N, double eps) {
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) {
+        const float* x = in + (int64_t)i * N;
+        double* y = out + (int64_t)i * N;
+        double mean = 0.0, var = 0.0;
+        for (int j = 0; j < N; ++j) mean += x[j];
+        mean /= N;
+        for (int j = 0; j < N; ++j) var += ((double)x[j] - mean) * ((double)x[j] - mean);
+        var /= N;
+        const double r = 1.0 / sqrt(var + eps);
+        for (int j = 0; j < N; ++j) y[j] = ((double)x[j] - mean) * r * gamma[j] + beta[j];
+    }
+}
+
+double jo64_cross_entropy(const float* logits, const int32_t* targets, double* grad, int M,
+                          int N) {
+    double total = 0.0;
+    jo64_softmax(grad, logits, M, N);
+    for (int i = 0; i < M; ++i) {
+        double* g = grad + (int64_t)i * N;
+        total += -log(g[targets[i]] + 1e-10);
+        g[targets[i]] -= 1.0;
+        for (int j = 0; j < N; ++j) g[j] /= M;
+    }
+    return total / M;
+}

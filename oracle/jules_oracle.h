@@ -38,6 +38,13 @@
  *                      invariance; S=1 and ragged S
  *   jo_matmul_int8     exact int64 numpy reference; one-hot KAT
  *   jo_w8a16           numpy fp64; one-hot KAT (bit-exact dequant)
+ *   jo_softmax         fp64 softmax; rows sum to 1; shift invariance; uniform
+ *                      rows give 1/N; N = 1; the 16-lane/tail split at N = 15,
+ *                      16, 17, 31, 33
+ *   jo_layernorm       fp64 layernorm; constant rows give beta; gamma = 1,
+ *                      beta = 0 rows have mean 0 and variance var/(var+eps)
+ *   jo_cross_entropy   fp64 loss and gradient; uniform logits give log N;
+ *                      gradient rows sum to 0; grad[target] = (p - 1)/M
  *   jo64_*             independent numpy fp64 implementations at small sizes
  * The reference itself cannot be compiled in this image (its headers include
  * <cblas.h>, which the image lacks), so no function is pinned against
@@ -129,6 +136,18 @@ void jo64_w8a16(const float* x, const int8_t* W, const float* scale,
                 const float* bias, double* y, int M, int N, int K, int act);
 
 /* threads the OpenMP runtime will use (for reporting the CPU baseline) */
+/* ---- row kernels (reference FusedKernels.h:464-526, :532-600, :766-854) ---- */
+void  jo_softmax(float* out, const float* in, int M, int N);
+void  jo_layernorm(float* out, const float* in, const float* gamma,
+                   const float* beta, int M, int N, float eps);
+float jo_cross_entropy(const float* logits, const int32_t* targets, float* grad,
+                       int M, int N);
+void   jo64_softmax(double* out, const float* in, int M, int N);
+void   jo64_layernorm(double* out, const float* in, const float* gamma,
+                      const float* beta, int M, int N, double eps);
+double jo64_cross_entropy(const float* logits, const int32_t* targets,
+                          double* grad, int M, int N);
+
 int jo_max_threads(void);
 void jo_set_threads(int n);
 

@@ -58,6 +58,13 @@ def lib():
             "jo64_attention_head": (None, [_f32p, _f32p, _f32p, _f64p, _c_int, _c_int,
                                            _c_int, ctypes.c_double, _i32p, _c_int]),
             "jo64_w8a16": (None, [_f32p, _i8p, _f32p, _f32p, _f64p] + [_c_int] * 4),
+            "jo_softmax": (None, [_f32p, _f32p, _c_int, _c_int]),
+            "jo_layernorm": (None, [_f32p, _f32p, _f32p, _f32p, _c_int, _c_int, ctypes.c_float]),
+            "jo_cross_entropy": (ctypes.c_float, [_f32p, _i32p, _f32p, _c_int, _c_int]),
+            "jo64_softmax": (None, [_f64p, _f32p, _c_int, _c_int]),
+            "jo64_layernorm": (None, [_f64p, _f32p, _f32p, _f32p, _c_int, _c_int,
+                                      ctypes.c_double]),
+            "jo64_cross_entropy": (ctypes.c_double, [_f32p, _i32p, _f64p, _c_int, _c_int]),
             "jo_max_threads": (_c_int, []),
             "jo_set_threads": (None, [_c_int]),
         }
@@ -241,6 +248,64 @@ def w8a16_64(x, W, scale, bias, act):
     lib().jo64_w8a16(_p(x, ctypes.c_float), _p(W, ctypes.c_int8), _p(scale, ctypes.c_float),
                      _p(bias, ctypes.c_float), _p(out, ctypes.c_double), M, N, K, act_code(act))
     return out
+
+
+# ---- row kernels (reference FusedKernels.h:464-526, :532-600, :766-854) ----
+def softmax(x):
+    """fusedSoftmax restated (AVX-512 path) over the rows of a 2-D array."""
+    x = _f32(x)
+    M, N = x.shape
+    out = np.empty_like(x)
+    lib().jo_softmax(_p(out, ctypes.c_float), _p(x, ctypes.c_float), M, N)
+    return out
+
+
+def softmax64(x):
+    x = _f32(x)
+    M, N = x.shape
+    out = np.empty((M, N), np.float64)
+    lib().jo64_softmax(_p(out, ctypes.c_double), _p(x, ctypes.c_float), M, N)
+    return out
+
+
+def layernorm(x, gamma, beta, eps=1e-5):
+    """fusedLayerNorm restated (AVX-512 path)."""
+    x, gamma, beta = _f32(x), _f32(gamma), _f32(beta)
+    M, N = x.shape
+    out = np.empty_like(x)
+    lib().jo_layernorm(_p(out, ctypes.c_float), _p(x, ctypes.c_float), _p(gamma, ctypes.c_float),
+                       _p(beta, ctypes.c_float), M, N, float(eps))
+    return out
+
+
+def layernorm64(x, gamma, beta, eps=1e-5):
+    x, gamma, beta = _f32(x), _f32(gamma), _f32(beta)
+    M, N = x.shape
+    out = np.empty((M, N), np.float64)
+    lib().jo64_layernorm(_p(out, ctypes.c_double), _p(x, ctypes.c_float),
+                         _p(gamma, ctypes.c_float), _p(beta, ctypes.c_float), M, N, float(eps))
+    return out
+
+
+def cross_entropy(logits, targets):
+    """fusedCrossEntropyLoss restated (AVX-512 path): (mean loss, grad)."""
+    x = _f32(logits)
+    t = np.ascontiguousarray(targets, np.int32)
+    M, N = x.shape
+    grad = np.empty_like(x)
+    loss = lib().jo_cross_entropy(_p(x, ctypes.c_float), _p(t, ctypes.c_int32),
+                                  _p(grad, ctypes.c_float), M, N)
+    return float(loss), grad
+
+
+def cross_entropy64(logits, targets):
+    x = _f32(logits)
+    t = np.ascontiguousarray(targets, np.int32)
+    M, N = x.shape
+    grad = np.empty((M, N), np.float64)
+    loss = lib().jo64_cross_entropy(_p(x, ctypes.c_float), _p(t, ctypes.c_int32),
+                                    _p(grad, ctypes.c_double), M, N)
+    return float(loss), grad
 
 
 def max_threads():

@@ -42,7 +42,8 @@ def test_cxx_shim_symbols_exported():
     exported = _exported()
     text = open(CXX_HEADER).read()
     names = ["fusedMatmulRelu", "fusedMatmulBiasRelu", "tiledMatmulWithActivation", "fusedGelu",
-             "matmulInt8", "flashAttention", "attention", "standardAttention", "lastStatus"]
+             "matmulInt8", "flashAttention", "attention", "standardAttention", "lastStatus",
+             "fusedSoftmax", "fusedLayerNorm", "fusedCrossEntropyLoss"]
     for n in names:
         assert re.search(rf"\b{n}\s*\(", text), n
         mangled = f"_ZN5jules6kernel{len(n)}{n}E"
@@ -62,7 +63,8 @@ def test_registry_names():
     names = _lib.kernel_names()
     routed = ["fusedMatmulRelu", "fusedMatmulSigmoid", "fusedMatmulTanh", "fusedMatmulGelu",
               "fusedMatmulBiasRelu", "fusedMatmulBiasSigmoid", "fusedMatmulBiasTanh",
-              "fusedGelu", "matmulInt8", "flashAttention"]
+              "fusedGelu", "matmulInt8", "flashAttention", "fusedSoftmax", "fusedLayerNorm",
+              "fusedCrossEntropyLoss"]
     added = ["fusedMatmulBiasGelu", "flashAttentionCausal", "matmulW8A16BiasSilu"]
     for n in routed + added:
         assert n in names
@@ -157,3 +159,21 @@ def test_registry_descriptor_validation():
     for x in list(t) + list(o):
         x.rank = 3
     assert fn(3, t, 1, o, None, None) == SHAPE
+
+
+def test_rowops_validation():
+    """Row kernels reject bad arguments before touching the device."""
+    L = _lib.lib()
+    assert L.jules_hip_softmax(None, None, -1, 4, None) == 2        # shape
+    assert L.jules_hip_softmax(None, None, 0, 4, None) == 0         # empty: no work
+    assert L.jules_hip_softmax(None, None, 4, 4, None) == 1         # null
+    assert L.jules_hip_softmax(2, 2, 4, 4, None) == 4               # misaligned (rejected before any launch)
+    assert L.jules_hip_layernorm(None, None, None, None, 2, 3, float("nan"), None) == 10
+    assert L.jules_hip_layernorm(None, None, None, None, 2, 3, -1.0, None) == 10
+    assert L.jules_hip_layernorm(None, None, None, None, 2, 3, 1e-5, None) == 1
+    assert L.jules_hip_cross_entropy_workspace_size(10) == 40
+    assert L.jules_hip_cross_entropy_workspace_size(0) == 4
+    assert L.jules_hip_cross_entropy(None, None, None, None, 3, 0, None, 0, None) == 2
+    assert L.jules_hip_cross_entropy(None, None, None, None, 3, 5, None, 0, None) == 1
+    assert L.jules_hip_cross_entropy(16, 16, 16, 16, 3, 5, None, 0, None) == 6   # workspace
+    assert L.jules_hip_cross_entropy(16, 16, 16, 16, 3, 5, 16, 8, None) == 6

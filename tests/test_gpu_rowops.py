@@ -1,0 +1,139 @@
+"""GPU parity of the row kernels: jules_hip_softmax, jules_hip_layernorm and
+jules_hip_cross_entropy (reference FusedKernels.h:464-526, :532-600,
+:766-854), fp32.
+
+Each is compared with the fp64 oracle at the fp32 bar (1e-5, normwise) and
+with the restated reference path to rounding (the GPU sums in a fixed tree
+order instead of the reference's 16 lane partials).  Shapes cover the
+reference's own benchmark shapes (softmax [64,256], [64,10], [2048,2048];
+layernorm [64,256], [2048,256]), the 16-element vector/tail split (N = 15,
+16, 17, 33), N = 1, ragged M, rows held in registers at every cache size,
+and rows longer than 4096 (the streaming passes)."""
+import numpy as np
+import pytest
+import torch
+
+from jules_amd import _lib, ops
+from oracle import inputs as I
+from oracle import pyoracle as po
+from tests.helpers import case, registry_call, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(64, 256), (64, 10), (2048, 2048), (2048, 256), (1, 1), (3, 15), (5, 16), (7, 17),
+          (9, 33), (13, 100), (6, 600), (5, 1500), (3, 4000), (3, 4096), (2, 4097), (2, 10000)]
+
+
+def _x(M, N, seed, scale=3.0):
+    return (np.random.default_rng(seed).standard_normal((M, N)) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,N", SHAPES)
+def test_softmax(dev, M, N):
+    case(f"softmax [{M},{N}]")
+    x = _x(M, N, M * 31 + N)
+    y = to_np(ops.softmax(to_dev(x, torch.float32, dev)))
+    assert I.rel_err(y, po.softmax64(x)) < I.TOL["f32"]
+    assert I.rel_err(y, po.softmax(x)) < 2e-6
+    assert np.abs(y.astype(np.float64).sum(1) - 1.0).max() < 1e-5
+
+
+def test_softmax_in_place_and_extremes(dev):
+    case("softmax in place, large and -inf logits")
+    x = _x(16, 300, 5, scale=40.0)
+    x[3, :] = -np.inf
+    x[3, 7] = 0.0                      # one finite logit: that entry is 1
+    x[4, :] = 1e30                     # all equal, huge: uniform
+    t = to_dev(x, torch.float32, dev)
+    ops.softmax(t, out=t)
+    y = to_np(t)
+    assert I.rel_err(y, po.softmax(x)) < 2e-6
+    assert y[3, 7] == 1.0 and np.all(np.delete(y[3], 7) == 0.0)
+    np.testing.assert_allclose(y[4], 1.0 / 300, rtol=1e-6)
+
+
+@pytest.mark.parametrize("M,N", SHAPES)
+def test_layernorm(dev, M, N):
+    case(f"layernorm [{M},{N}]")
+    x = _x(M, N, M * 17 + N, scale=2.0) + np.float32(0.75)
+    rng = np.random.default_rng(N)
+    g = rng.standard_normal(N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    y = to_np(ops.layernorm(to_dev(x, torch.float32, dev), to_dev(g, torch.float32, dev),
+                            to_dev(b, torch.float32, dev)))
+    assert I.rel_err(y, po.layernorm64(x, g, b)) < I.TOL["f32"]
+    assert I.rel_err(y, po.layernorm(x, g, b)) < 2e-6
+
+
+def test_layernorm_epsilon_and_constant_rows(dev):
+    case("layernorm epsilon, constant rows")
+    N = 96
+    x = _x(8, N, 9)
+    x[2, :] = 5.0                      # constant row -> beta exactly
+    g = np.full(N, 1.5, np.float32)
+    b = np.linspace(-1, 1, N).astype(np.float32)
+    for eps in (1e-5, 0.1, 0.0):
+        y = to_np(ops.layernorm(to_dev(x, torch.float32, dev), to_dev(g, torch.float32, dev),
+                                to_dev(b, torch.float32, dev), eps=eps))
+        ok = np.arange(8) != 2 if eps == 0.0 else np.ones(8, bool)
+        assert I.rel_err(y[ok], po.layernorm64(x, g, b, eps)[ok]) < I.TOL["f32"]
+        if eps > 0:
+            assert np.array_equal(y[2], b)
+
+
+@pytest.mark.parametrize("M,N", [(64, 10), (128, 1000), (7, 17), (1, 1), (5, 4096), (3, 7000),
+                                 (2048, 512)])
+def test_cross_entropy(dev, M, N):
+    case(f"cross entropy [{M},{N}]")
+    x = _x(M, N, 3 * M + N)
+    t = np.random.default_rng(M + N).integers(0, N, M).astype(np.int32)
+    t[0] = N - 1
+    loss, g = ops.cross_entropy(to_dev(x, torch.float32, dev), to_dev(t, torch.int32, dev))
+    loss, g = float(to_np(loss)[0]), to_np(g)
+    loss64, g64 = po.cross_entropy64(x, t)
+    assert abs(loss - loss64) <= I.TOL["f32"] * max(1.0, abs(loss64))
+    assert I.rel_err(g, g64) < I.TOL["f32"]
+    lr, gr = po.cross_entropy(x, t)
+    assert I.rel_err(g, gr) < 2e-6
+    assert abs(loss - lr) <= 2e-6 * max(1.0, abs(lr))
+
+
+def test_cross_entropy_bad_target_and_repeat(dev):
+    """An out-of-range target gives a NaN loss (the reference reads out of
+    bounds); the workspace is reused across calls without stale data."""
+    case("cross entropy bad target, repeated calls")
+    x = _x(6, 50, 1)
+    t = np.array([0, 49, 3, 3, 10, 20], np.int32)
+    xt, ws = to_dev(x, torch.float32, dev), ops.cross_entropy_workspace(6, dev)
+    l1, _ = ops.cross_entropy(xt, to_dev(t, torch.int32, dev), workspace=ws)
+    bad = t.copy()
+    bad[2] = 50
+    l2, g2 = ops.cross_entropy(xt, to_dev(bad, torch.int32, dev), workspace=ws)
+    l3, _ = ops.cross_entropy(xt, to_dev(t, torch.int32, dev), workspace=ws)
+    assert np.isfinite(float(to_np(l1)[0])) and np.isnan(float(to_np(l2)[0]))
+    assert float(to_np(l1)[0]) == float(to_np(l3)[0])
+    # the bad row's gradient is the plain softmax / M (no onehot subtraction)
+    np.testing.assert_allclose(to_np(g2)[2], po.softmax(x)[2] / 6, rtol=2e-6)
+
+
+def test_registry_row_kernels(dev):
+    """fusedSoftmax / fusedLayerNorm / fusedCrossEntropyLoss through jules_hip_lookup."""
+    case("registry row kernels")
+    x = _x(12, 80, 2)
+    xt = to_dev(x, torch.float32, dev)
+    y = torch.empty_like(xt)
+    st = registry_call("fusedSoftmax", [xt], [y])
+    assert st == 0, _lib.lib().jules_hip_last_error()
+    assert I.rel_err(to_np(y), po.softmax64(x)) < I.TOL["f32"]
+    g = to_dev(np.full(80, 2.0, np.float32), torch.float32, dev)
+    b = to_dev(np.full(80, -1.0, np.float32), torch.float32, dev)
+    st = registry_call("fusedLayerNorm", [xt, g, b], [y], b"epsilon=0.5")
+    assert st == 0, _lib.lib().jules_hip_last_error()
+    assert I.rel_err(to_np(y), po.layernorm64(x, np.full(80, 2.0), np.full(80, -1.0), 0.5)) < I.TOL["f32"]
+    t = to_dev(np.arange(12, dtype=np.int32) * 5, torch.int32, dev)
+    loss = torch.empty((1,), dtype=torch.float32, device=dev)
+    st = registry_call("fusedCrossEntropyLoss", [xt, t], [y, loss])
+    assert st == 0, _lib.lib().jules_hip_last_error()
+    l64, g64 = po.cross_entropy64(x, np.arange(12, dtype=np.int32) * 5)
+    assert abs(float(to_np(loss)[0]) - l64) < 1e-5 * max(1, abs(l64))
+    assert I.rel_err(to_np(y), g64) < I.TOL["f32"]

@@ -323,3 +323,90 @@ def test_rel_err_metric():
     o = np.array([1.0, -4.0, 2.0])
     assert I.rel_err(o, o) == 0.0
     assert I.rel_err(o + np.array([0, 0.4, 0]), o) == pytest.approx(0.1)
+
+
+# ---- row kernels (reference FusedKernels.h:464-526, :532-600, :766-854) ----
+ROW_SHAPES = [(3, 1), (4, 10), (5, 15), (5, 16), (5, 17), (4, 31), (4, 33), (8, 256), (3, 1000)]
+
+
+def _rows(M, N, seed, scale=3.0):
+    return (np.random.default_rng(seed).standard_normal((M, N)) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,N", ROW_SHAPES)
+def test_softmax_against_fp64_and_invariants(M, N):
+    x = _rows(M, N, M * 100 + N)
+    y = po.softmax(x)
+    y64 = po.softmax64(x)
+    assert I.rel_err(y, y64) < 2e-6
+    assert np.abs(y.astype(np.float64).sum(1) - 1.0).max() < 2e-6
+    # shift invariance: the row max is subtracted first
+    y2 = po.softmax(x + np.float32(7.0))
+    assert I.rel_err(y2, y64) < 5e-6
+    # a uniform row gives exactly 1/N's rounding: every entry equal
+    u = po.softmax(np.full((2, N), 0.25, np.float32))
+    assert np.all(u == u[0, 0]) and abs(float(u[0, 0]) - 1.0 / N) < 1e-6 / N * 4
+
+
+def test_softmax_split_between_fast_exp_and_expf():
+    """Elements j < N & ~15 use fast_exp, the tail libm expf (reference :484-497)."""
+    N = 20
+    x = _rows(1, N, 7)
+    y = po.softmax(x)
+    mx = x.max()
+    fe = po.fast_exp(x[0, :16] - mx)
+    tail = np.exp((x[0, 16:] - mx).astype(np.float32))
+    e = np.concatenate([fe, tail.astype(np.float32)])
+    np.testing.assert_allclose(y[0], e / e.astype(np.float64).sum(), rtol=2e-6)
+    # fast_exp is not libm exp: the restatement must be using it on the vector part
+    assert np.any(fe != np.exp(x[0, :16] - mx).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N", ROW_SHAPES)
+def test_layernorm_against_fp64_and_closed_forms(M, N):
+    x = _rows(M, N, M * 7 + N, scale=2.0) + np.float32(1.5)
+    rng = np.random.default_rng(N)
+    g = rng.standard_normal(N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    y = po.layernorm(x, g, b)
+    assert I.rel_err(y, po.layernorm64(x, g, b)) < 2e-6
+    # gamma = 1, beta = 0: zero mean, variance var / (var + eps)
+    ones, zeros = np.ones(N, np.float32), np.zeros(N, np.float32)
+    z = po.layernorm(x, ones, zeros).astype(np.float64)
+    var = x.astype(np.float64).var(1)
+    if N > 1:
+        assert np.abs(z.mean(1)).max() < 1e-5
+        np.testing.assert_allclose(z.var(1), var / (var + 1e-5), rtol=1e-5)
+    # a constant row normalises to beta exactly
+    c = po.layernorm(np.full((2, N), 3.25, np.float32), g, b)
+    assert np.array_equal(c, np.broadcast_to(b, (2, N)))
+
+
+def test_layernorm_planted_mistake_is_caught():
+    """A slip that forgets the epsilon or uses the sample variance fails the fp64 check."""
+    x = _rows(4, 33, 3)
+    g, b = np.ones(33, np.float32), np.zeros(33, np.float32)
+    y = po.layernorm(x, g, b)
+    m = x.mean(1, keepdims=True)
+    wrong = (x - m) / np.sqrt(x.var(1, ddof=1, keepdims=True) + 1e-5)
+    assert I.rel_err(wrong.astype(np.float32), po.layernorm64(x, g, b)) > 1e-3
+    assert I.rel_err(y, po.layernorm64(x, g, b)) < 2e-6
+
+
+@pytest.mark.parametrize("M,N", [(1, 1), (4, 10), (5, 17), (8, 256), (3, 1000)])
+def test_cross_entropy_against_fp64_and_invariants(M, N):
+    x = _rows(M, N, 11 * M + N)
+    t = np.random.default_rng(N).integers(0, N, M).astype(np.int32)
+    t[0] = N - 1
+    loss, g = po.cross_entropy(x, t)
+    loss64, g64 = po.cross_entropy64(x, t)
+    assert abs(loss - loss64) <= 2e-6 * max(1.0, abs(loss64))
+    assert I.rel_err(g, g64) < 2e-6
+    # gradient rows sum to 0; grad[target] = (p - 1) / M
+    assert np.abs(g.astype(np.float64).sum(1)).max() < 1e-6
+    p = po.softmax(x)
+    np.testing.assert_allclose(g[np.arange(M), t], (p[np.arange(M), t] - 1.0) / M, rtol=1e-6,
+                               atol=1e-9)
+    # uniform logits: loss = log N (up to the 1e-10 guard)
+    lu, _ = po.cross_entropy(np.zeros((M, N), np.float32), t)
+    assert abs(lu - np.log(N)) < 1e-5 * max(1.0, np.log(N)) + 1e-6
