@@ -7,9 +7,11 @@ flash-attention forward at [8,32,4096,128] (config 4), on device-resident
 synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 (2*M*N*K + 4*B*H*D*S*(S+1)/2 FLOP per step) over the timed steps.
 
-The same run also times every BASELINE config on its own (per_config), the
-dominant kernel against its roofline (roofline), and the CPU port of the
-reference AVX-512 path on a bounded sample (cpu_baseline).
+The same run also times every BASELINE config on its own (per_config, keys
+c1-c5), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
+entropy, GB/s against HBM), the dominant kernel against its roofline
+(roofline), and the CPU port of the reference AVX-512 path on a bounded
+sample (cpu_baseline).
 
   python bench.py [--steps K] [--warmup W] [--no-cpu] [--only c1,c3,...]
 """
@@ -58,6 +60,26 @@ CONFIGS = {
     "c5": dict(kind="w8a16", M=8, N=8192, K=8192, act="silu"),
 }
 
+# Row kernels (the next rows of the hot-path scope; not BASELINE configs):
+# the reference's own benchmark shapes (bench_kernel.cpp:396-399, :450-453)
+# and one large shape each, where launch latency does not dominate.
+ROW_CONFIGS = {
+    "r1": dict(kind="softmax", M=2048, N=2048),
+    "r2": dict(kind="softmax", M=16384, N=4096),
+    "r3": dict(kind="layernorm", M=2048, N=256),
+    "r4": dict(kind="layernorm", M=16384, N=4096),
+    "r5": dict(kind="xent", M=16384, N=4096),
+    "r6": dict(kind="xent", M=4096, N=32000),
+}
+
+
+def row_bytes(spec):
+    """Algorithmic HBM bytes: the fp32 rows read once and written once, plus
+    gamma/beta (layernorm) or targets and the loss (cross entropy)."""
+    M, N = spec["M"], spec["N"]
+    extra = {"softmax": 0, "layernorm": 8 * N, "xent": 4 * M + 4}[spec["kind"]]
+    return 8 * M * N + extra
+
 
 class Runner:
     """Inputs of one config resident in HBM and a launch() of its kernel."""
@@ -97,6 +119,19 @@ class Runner:
             self.work = flash_flops(B, H, S, D, s["causal"])
             self.unit, self.bound = "TFLOP/s", "mfma"
             self.peak = PEAK["bf16"] if s["dtype"] == "bf16" else PEAK["f32"]
+        elif s["kind"] in ("softmax", "layernorm", "xent"):
+            M, N = s["M"], s["N"]
+            self.x = torch.randn((M, N), generator=g, device=dev) * 3
+            self.y = torch.empty_like(self.x)
+            if s["kind"] == "layernorm":
+                self.gamma = torch.randn((N,), generator=g, device=dev)
+                self.beta = torch.randn((N,), generator=g, device=dev)
+            if s["kind"] == "xent":
+                self.t = torch.randint(0, N, (M,), generator=g, device=dev, dtype=torch.int32)
+                self.loss = torch.empty((1,), device=dev)
+                self.ws = ops.cross_entropy_workspace(M, dev)
+            self.work = row_bytes(s)
+            self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK["hbm"]
         else:
             M, N, K = s["M"], s["N"], s["K"]
             # 64 MiB of weights fits in the 256 MB MALL: rotate 8 distinct
@@ -119,6 +154,12 @@ class Runner:
             ops.gemm_bias_act(self.A, self.B, self.bias, s["act"], out=self.C)
         elif s["kind"] == "flash":
             ops.flash_attention(self.Q, self.K, self.V, s["causal"], self.scale, out=self.O)
+        elif s["kind"] == "softmax":
+            ops.softmax(self.x, out=self.y)
+        elif s["kind"] == "layernorm":
+            ops.layernorm(self.x, self.gamma, self.beta, out=self.y)
+        elif s["kind"] == "xent":
+            ops.cross_entropy(self.x, self.t, grad=self.y, loss=self.loss, workspace=self.ws)
         else:
             ops.w8a16_gemm(self.x, self.W[self.i % self.nw], self.scale, self.bias, s["act"],
                            out=self.y, workspace=self.ws)
@@ -272,20 +313,21 @@ def main():
 
     # ---- per-config launch timings -----------------------------------------
     per = {}
-    names = [n for n in CONFIGS if not args.only or n in args.only.split(",")]
+    ALL = {**CONFIGS, **ROW_CONFIGS}
+    names = [n for n in ALL if not args.only or n in args.only.split(",")]
     if args.step_only:
         names = []
     for name in names:
-        log(f"config {name} {CONFIGS[name]}")
+        log(f"config {name} {ALL[name]}")
         try:
-            r = Runner(name, CONFIGS[name], dev)
-            iters = 50 if name in ("c1", "c2", "c5") else 20
+            r = Runner(name, ALL[name], dev)
+            iters = 20 if name in ("c3", "c4") else 50
             durs, _ = time_launches([r], 5, iters)
             d = sorted(durs[0])
             med = statistics.median(d)
             per[name] = {"median_ms": med, "p10_ms": d[len(d) // 10], "p90_ms": d[(9 * len(d)) // 10],
                          "achieved": r.rate(med), "unit": r.unit, "peak": r.peak,
-                         "frac": r.rate(med) / r.peak, "work": r.work, "spec": CONFIGS[name]}
+                         "frac": r.rate(med) / r.peak, "work": r.work, "spec": ALL[name]}
             del r
         except Exception as e:  # report and continue
             per[name] = {"error": f"{type(e).__name__}: {e}"}

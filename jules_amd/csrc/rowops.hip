@@ -16,9 +16,13 @@
 // All three are HBM-bound.  One wave owns a row; with N <= 4096 the row is
 // held in registers (ELEMS elements per lane, element j = lane + 64 * t, so
 // every load and store instruction covers 256 contiguous bytes), read from
-// HBM once and written once.  Longer rows take three streaming passes, the
-// reference's own pass structure.  Four rows per workgroup; the wave
-// reductions are a fixed butterfly, so results are deterministic.
+// HBM once and written once, four rows per workgroup.  Longer rows get a
+// 256-thread workgroup each and three passes over the row (max, sum, write:
+// the reference's own pass structure, with the exponentials recomputed in the
+// last pass instead of stored); the loads of a pass are unrolled four deep
+// and the re-reads of a row mostly hit the MALL.  Reductions are a fixed
+// butterfly within a wave and a fixed order across waves, so results are
+// deterministic.
 #include <cfloat>
 
 #include "common.hpp"
@@ -97,28 +101,60 @@ __global__ __launch_bounds__(256) void softmax_kernel(float* __restrict__ out,
     }
 }
 
-// rows longer than MAX_CACHED: max pass, exp + sum pass (e stored in out),
-// normalize pass - the reference's passes 1a, 1b, 2
-__global__ __launch_bounds__(256) void softmax_stream_kernel(float* out, const float* in, int M,
-                                                             int N) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const float* x = in + (int64_t)row * N;
-    float* y = out + (int64_t)row * N;
+// ---- rows longer than MAX_CACHED: one 256-thread workgroup per row ----
+constexpr int LT = 256;  // threads per long row
+
+// fixed-order reductions over the workgroup (4 waves)
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();  // red is reused by consecutive reductions
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// f(j) for j = tid, tid + 256, ... < N, four loads in flight
+template <typename F>
+__device__ __forceinline__ void row_loop(int N, F&& f) {
+    int j = threadIdx.x;
+    for (; j + 3 * LT < N; j += 4 * LT) {
+        f(j);
+        f(j + LT);
+        f(j + 2 * LT);
+        f(j + 3 * LT);
+    }
+    for (; j < N; j += LT) f(j);
+}
+
+// max and sum of exp(x - max) of a long row (reference passes 1a and 1b)
+__device__ __forceinline__ void long_row_stats(const float* x, int N, float* red, float* mx_out,
+                                               float* s_out) {
     const int nv = N & ~15;
     float mx = -FLT_MAX;
-    for (int j = lane; j < N; j += 64) mx = ref_max(mx, x[j]);
-    mx = wave_max(mx);
+    row_loop(N, [&](int j) { mx = ref_max(mx, x[j]); });
+    mx = block_max(mx, red);
     float s = 0.0f;
-    for (int j = lane; j < N; j += 64) {
-        const float e = row_exp(x[j] - mx, j, nv);
-        y[j] = e;
-        s += e;
-    }
-    s = wave_sum(s);
+    row_loop(N, [&](int j) { s += row_exp(x[j] - mx, j, nv); });
+    *mx_out = mx;
+    *s_out = block_sum(s, red);
+}
+
+__global__ __launch_bounds__(LT) void softmax_long_kernel(float* out, const float* in, int N) {
+    __shared__ float red[4];
+    const float* x = in + (int64_t)blockIdx.x * N;
+    float* y = out + (int64_t)blockIdx.x * N;
+    const int nv = N & ~15;
+    float mx, s;
+    long_row_stats(x, N, red, &mx, &s);
     const float inv = 1.0f / s;
-    for (int j = lane; j < N; j += 64) y[j] = row_norm(y[j], inv, s, j, nv);
+    row_loop(N, [&](int j) { y[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv); });
 }
 
 // ---- layernorm ----
@@ -158,26 +194,24 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float* __restrict__ out,
     }
 }
 
-__global__ __launch_bounds__(256) void layernorm_stream_kernel(float* out, const float* in,
-                                                               const float* __restrict__ gamma,
-                                                               const float* __restrict__ beta,
-                                                               int M, int N, float eps) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const float* x = in + (int64_t)row * N;
-    float* y = out + (int64_t)row * N;
+__global__ __launch_bounds__(LT) void layernorm_long_kernel(float* out, const float* in,
+                                                           const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta, int N,
+                                                           float eps) {
+    __shared__ float red[4];
+    const float* x = in + (int64_t)blockIdx.x * N;
+    float* y = out + (int64_t)blockIdx.x * N;
     float s = 0.0f;
-    for (int j = lane; j < N; j += 64) s += x[j];
-    const float mean = wave_sum(s) / (float)N;
+    row_loop(N, [&](int j) { s += x[j]; });
+    const float mean = block_sum(s, red) / (float)N;
     float q = 0.0f;
-    for (int j = lane; j < N; j += 64) {
+    row_loop(N, [&](int j) {
         const float d = x[j] - mean;
         q = __builtin_fmaf(d, d, q);
-    }
-    const float var = wave_sum(q) / (float)N;
+    });
+    const float var = block_sum(q, red) / (float)N;
     const float inv_std = 1.0f / sqrtf(var + eps);
-    for (int j = lane; j < N; j += 64) y[j] = __builtin_fmaf((x[j] - mean) * inv_std, gamma[j], beta[j]);
+    row_loop(N, [&](int j) { y[j] = __builtin_fmaf((x[j] - mean) * inv_std, gamma[j], beta[j]); });
 }
 
 // ---- cross entropy: grad rows and per-row losses (row_loss[M]) ----
@@ -217,37 +251,28 @@ __global__ __launch_bounds__(256) void cross_entropy_kernel(const float* __restr
     if (lane == 0) row_loss[row] = valid ? -logf(pt + 1e-10f) : __builtin_nanf("");
 }
 
-__global__ __launch_bounds__(256) void cross_entropy_stream_kernel(const float* logits,
-                                                                   const int32_t* targets,
-                                                                   float* grad, float* row_loss,
-                                                                   int M, int N) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-    if (row >= M) return;
+__global__ __launch_bounds__(LT) void cross_entropy_long_kernel(const float* logits,
+                                                               const int32_t* targets, float* grad,
+                                                               float* row_loss, int M, int N) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
     const float* x = logits + (int64_t)row * N;
     float* g = grad + (int64_t)row * N;
     const int nv = N & ~15;
-    float mx = -FLT_MAX;
-    for (int j = lane; j < N; j += 64) mx = ref_max(mx, x[j]);
-    mx = wave_max(mx);
-    float s = 0.0f;
-    for (int j = lane; j < N; j += 64) {
-        const float e = row_exp(x[j] - mx, j, nv);
-        g[j] = e;
-        s += e;
-    }
-    s = wave_sum(s);
+    float mx, s;
+    long_row_stats(x, N, red, &mx, &s);
     const float inv = 1.0f / s;
     const int t = targets[row];
     const bool valid = t >= 0 && t < N;
+    const float fm = (float)M;
     float pt = 0.0f;
-    for (int j = lane; j < N; j += 64) {
-        const float p = row_norm(g[j], inv, s, j, nv);
+    row_loop(N, [&](int j) {
+        const float p = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv);
         if (j == t) pt = p;
-        g[j] = ce_grad(p, j, valid ? t : -1, (float)M);
-    }
-    pt = wave_sum(pt);
-    if (lane == 0) row_loss[row] = valid ? -logf(pt + 1e-10f) : __builtin_nanf("");
+        g[j] = ce_grad(p, j, valid ? t : -1, fm);
+    });
+    pt = block_sum(pt, red);  // one thread holds it, the others 0
+    if (threadIdx.x == 0) row_loss[row] = valid ? -logf(pt + 1e-10f) : __builtin_nanf("");
 }
 
 // loss = sum of row_loss in a fixed order / M (one workgroup)
@@ -279,7 +304,7 @@ hipError_t by_elems(int N, F&& f) {
 hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t s) {
     const unsigned blocks = (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
     if (N > MAX_CACHED) {
-        hipLaunchKernelGGL(softmax_stream_kernel, dim3(blocks), dim3(256), 0, s, out, in, M, N);
+        hipLaunchKernelGGL(softmax_long_kernel, dim3(M), dim3(LT), 0, s, out, in, N);
         return hipGetLastError();
     }
     return by_elems(N, [&](auto e) {
@@ -293,8 +318,8 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
                             int M, int N, float eps, hipStream_t s) {
     const unsigned blocks = (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
     if (N > MAX_CACHED) {
-        hipLaunchKernelGGL(layernorm_stream_kernel, dim3(blocks), dim3(256), 0, s, out, in, gamma,
-                           beta, M, N, eps);
+        hipLaunchKernelGGL(layernorm_long_kernel, dim3(M), dim3(LT), 0, s, out, in, gamma, beta, N,
+                           eps);
         return hipGetLastError();
     }
     return by_elems(N, [&](auto e) {
@@ -309,8 +334,9 @@ hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, flo
     const unsigned blocks = (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
     hipError_t e;
     if (N > MAX_CACHED) {
-        hipLaunchKernelGGL(cross_entropy_stream_kernel, dim3(blocks), dim3(256), 0, s, logits,
-                           targets, grad, row_loss, M, N);
+        if (M > 0)
+            hipLaunchKernelGGL(cross_entropy_long_kernel, dim3(M), dim3(LT), 0, s, logits, targets,
+                               grad, row_loss, M, N);
         e = hipGetLastError();
     } else {
         e = by_elems(N, [&](auto el) {
