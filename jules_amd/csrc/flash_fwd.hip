@@ -248,7 +248,7 @@ __device__ __forceinline__ void flash_bf16_body(
     using C = Bf16Cfg<D>;
     constexpr int BKV = C::BKV;
     constexpr float kLazy = 8.0f;
-    constexpr int LA = 3;                       // MFMAs whose LDS reads are in flight
+    constexpr int LA = 7;                       // MFMAs whose LDS reads are in flight
     constexpr int KR = LA + 2, VR = LA + 2;     // K / V fragment ring sizes
     constexpr int PIECES = 2 * C::SEGW;         // copy instructions per wave per tile
     __shared__ __attribute__((aligned(1024))) uint8_t sm[C::NSTAGE * C::STAGE];
