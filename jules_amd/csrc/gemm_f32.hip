@@ -12,6 +12,8 @@
 //
 // Data path: A and B tiles are staged through LDS (A transposed to k-major so
 // a thread reads its TM rows as one vector), one barrier pair per BK slice.
+// The global loads of slice k+1 are issued into registers before slice k is
+// computed, so their latency is paid once per launch, not once per slice.
 // The K tail is handled by a uniform trip count, never by zero padding (an
 // extra fma(0, b, acc) could turn a -0 partial sum into +0).
 #include "common.hpp"
@@ -39,21 +41,44 @@ __global__ __launch_bounds__((BM / TM) * (BN / TN)) void gemm_f32_kernel(
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
 
+    constexpr int PA = (BM * BK + NT - 1) / NT;  // A elements per thread per slice
+    constexpr int PB = (BK * BN + NT - 1) / NT;
+    float ra[PA], rb[PB];
+    auto gload = [&](int k0) {
+        const int kc = min(BK, K - k0);
+#pragma unroll
+        for (int p = 0; p < PA; ++p) {
+            const int e = tid + p * NT;
+            const int m = e / BK, k = e % BK;
+            ra[p] = (e < BM * BK && m0 + m < M && k < kc) ? A[(int64_t)(m0 + m) * K + k0 + k] : 0.0f;
+        }
+#pragma unroll
+        for (int p = 0; p < PB; ++p) {
+            const int e = tid + p * NT;
+            const int k = e / BN, n = e % BN;
+            rb[p] = (e < BK * BN && k < kc && n0 + n < N) ? B[(int64_t)(k0 + k) * N + n0 + n] : 0.0f;
+        }
+    };
+    auto sstore = [&]() {
+#pragma unroll
+        for (int p = 0; p < PA; ++p) {
+            const int e = tid + p * NT;
+            if (e < BM * BK) As[e % BK][e / BK] = ra[p];
+        }
+#pragma unroll
+        for (int p = 0; p < PB; ++p) {
+            const int e = tid + p * NT;
+            if (e < BK * BN) Bs[e / BN][e % BN] = rb[p];
+        }
+    };
+
+    if (K > 0) gload(0);
     for (int k0 = 0; k0 < K; k0 += BK) {
         const int kc = min(BK, K - k0);
-        for (int e = tid; e < BM * BK; e += NT) {
-            const int m = e / BK, k = e % BK;
-            float v = 0.0f;
-            if (m0 + m < M && k < kc) v = A[(int64_t)(m0 + m) * K + k0 + k];
-            As[k][m] = v;
-        }
-        for (int e = tid; e < BK * BN; e += NT) {
-            const int k = e / BN, n = e % BN;
-            float v = 0.0f;
-            if (k < kc && n0 + n < N) v = B[(int64_t)(k0 + k) * N + n0 + n];
-            Bs[k][n] = v;
-        }
+        sstore();
         __syncthreads();
+        if (k0 + BK < K) gload(k0 + BK);
+#pragma unroll 8
         for (int k = 0; k < kc; ++k) {
             float a[TM], b[TN];
 #pragma unroll
@@ -110,9 +135,9 @@ hipError_t launch_gemm_f32(int act, const float* A, const float* B, const float*
     const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
     hipError_t e = hipSuccess;
     if (tiles64 >= 512) {
-        JH_DISPATCH_ACT(act, ACT, e = (run<64, 64, 16, 4, 4, ACT>(A, B, bias, C, M, N, K, s)));
+        JH_DISPATCH_ACT(act, ACT, e = (run<64, 64, 32, 4, 4, ACT>(A, B, bias, C, M, N, K, s)));
     } else {
-        JH_DISPATCH_ACT(act, ACT, e = (run<32, 32, 16, 2, 2, ACT>(A, B, bias, C, M, N, K, s)));
+        JH_DISPATCH_ACT(act, ACT, e = (run<32, 32, 32, 2, 2, ACT>(A, B, bias, C, M, N, K, s)));
     }
     return e;
 }
