@@ -20,15 +20,15 @@
 //     O^T = V^T P^T: for key step kk the 8 keys a lane holds are
 //     {16kk + 4g + 0..3, 16kk + 8 + 4g + 0..3} (g = lane / 32), which are
 //     accumulator elements 8*(kk%2) .. 8*(kk%2)+7 of score tile kk/2.
-// V^T must supply the same 8 keys per lane: V tiles are transposed into LDS
-// (d-major, keys contiguous) with the key order inside each 16-key group
-// stored as [0-3, 8-11, 4-7, 12-15], so each operand is one 16-byte read.
+// V^T must supply the same 8 keys per lane; the bf16 kernel reads it with
+// transposing LDS reads (ds_read_b64_tr_b16), the fp32 kernel needs no
+// transpose (see the per-kernel notes below).
 //
-// Block: 4 waves x 32 queries = 128 query rows; key tiles of 64 (bf16) or 32
-// (fp32) rows, double-buffered in LDS, loaded by the whole block.  Causal
-// blocks stop at the diagonal, waves skip key tiles that are wholly above
-// their own diagonal, and the heaviest query tiles of a head are dispatched
-// first; each XCD works through whole heads so K and V are re-read from L2.
+// Blocks: bf16 = 8 waves x 32 queries (256 rows) sharing K/V tiles of 64
+// keys; fp32 = 32 queries whose key range is split across 4 waves.  Causal
+// blocks stop at the diagonal, the heaviest query tiles of a head are
+// dispatched first, and each XCD works through whole heads so K and V are
+// re-read from its L2.
 //
 // bf16: v_mfma_f32_32x32x16_bf16, fp32 softmax statistics, exp2 with
 // scale*log2(e) folded into one fma.  fp32: v_mfma_f32_32x32x2_f32 (full fp32
@@ -41,8 +41,6 @@
 namespace jh {
 namespace {
 
-constexpr int BQ = 128;
-constexpr int NW = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -542,51 +540,69 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_bf16(
 // read from LDS as [key][d] rows without any transpose: for the PV product
 // k-step (j, i) pairs keys 8j+i (lanes 0-31) and 8j+4+i (lanes 32-63), which
 // are exactly the score accumulator element 4j+i each lane already holds.
+//
+// Work split: a workgroup owns 32 queries, and its 4 waves split the key
+// range (wave w takes key tiles w, w+4, ...), each with its own running
+// max, sum and accumulator; at the end the four partial states are merged
+// in LDS in a fixed order.  With causal masking the query groups near the
+// diagonal carry the longest key ranges; splitting the range bounds the
+// longest chain a single wave runs to a quarter of it.  Each wave stages its
+// own K/V tiles through a private LDS region (register prefetch of the next
+// tile while the current one is computed), so the main loop needs no
+// workgroup barrier.
 // ---------------------------------------------------------------------------
+constexpr int BQF = 32;  // query rows per fp32 workgroup
+constexpr int NWF = 4;   // waves per fp32 workgroup (key-range split)
+
 template <int D>
 struct F32Cfg {
     static constexpr int BKV = 32;
-    static constexpr int ROWF = D + 4;  // padded row (floats): rows shift by 16 B
+    static constexpr int ROWF = D + 4;                 // padded row (floats): rows shift by 16 B
     static constexpr int K_FLOATS = BKV * ROWF;
-    static constexpr int STAGE_FLOATS = 2 * K_FLOATS;  // K then V
-    static constexpr int CHUNKS = BKV * D / 4;         // 16-byte chunks per tile
+    static constexpr int WAVE_FLOATS = 2 * K_FLOATS;   // one wave's K then V tile
+    static constexpr int PT = BKV * D / 4 / 64;        // 16-byte chunks per lane per operand
 };
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void flash_fwd_f32(
+__device__ __forceinline__ void flash_f32_body(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int BH, int S, float c_log2) {
     using C = F32Cfg<D>;
     constexpr int BKV = C::BKV;
-    __shared__ __attribute__((aligned(16))) float smem[2 * C::STAGE_FLOATS];
+    // K/V stages during the loop; the merge reuses the same memory
+    constexpr int MERGE_FLOATS = NWF * (BQF * D + 2 * BQF);
+    constexpr int SMEM_FLOATS = NWF * C::WAVE_FLOATS > MERGE_FLOATS ? NWF * C::WAVE_FLOATS
+                                                                       : MERGE_FLOATS;
+    __shared__ __attribute__((aligned(16))) float smem[SMEM_FLOATS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
-    const int nq = (S + BQ - 1) / BQ;
+    const int nq = (S + BQF - 1) / BQF;
     int bh, q0;
-    block_coords(BH, nq, BQ, &bh, &q0);
+    block_coords(BH, nq, BQF, &bh, &q0);
     const int64_t hoff = (int64_t)bh * S * D;
     const float* Qh = Q + hoff;
     const float* Kh = K + hoff;
     const float* Vh = V + hoff;
-    const int qw0 = q0 + wave * 32;
-    const int qrow = qw0 + col;
+    const int qrow = q0 + col;
 
     float qf[D / 2];  // Q[qrow][2 ks + g]
 #pragma unroll
     for (int ks = 0; ks < D / 2; ++ks) qf[ks] = (qrow < S) ? Qh[(int64_t)qrow * D + 2 * ks + g] : 0.0f;
 
-    const int kv_end = CAUSAL ? min(S, q0 + BQ) : S;
+    const int kv_end = CAUSAL ? min(S, q0 + BQF) : S;
     const int n_kv = (kv_end + BKV - 1) / BKV;
-    constexpr int PT = (C::CHUNKS + 255) / 256;
-    f32x4_t rk[PT], rv[PT];
+
+    float* Ks = smem + wave * C::WAVE_FLOATS;  // this wave's tile
+    float* Vs = Ks + C::K_FLOATS;
+    f32x4_t rk[C::PT], rv[C::PT];
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            const int c = tid + 256 * i;
+        for (int i = 0; i < C::PT; ++i) {
+            const int c = lane + 64 * i;
             const int key = c / (D / 4), ch = c % (D / 4);
             f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-            if (c < C::CHUNKS && k0 + key < S) {
+            if (k0 + key < S) {
                 a = *reinterpret_cast<const f32x4_t*>(Kh + (int64_t)(k0 + key) * D + 4 * ch);
                 b = *reinterpret_cast<const f32x4_t*>(Vh + (int64_t)(k0 + key) * D + 4 * ch);
             }
@@ -594,17 +610,15 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_f32(
             rv[i] = b;
         }
     };
-    auto lstore = [&](int stage) {
-        float* Ks = smem + stage * C::STAGE_FLOATS;
-        float* Vs = Ks + C::K_FLOATS;
+    // the wave's LDS reads of the previous tile are issued before these
+    // writes and LDS operations of one wave execute in order
+    auto lstore = [&]() {
 #pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            const int c = tid + 256 * i;
-            if (c < C::CHUNKS) {
-                const int key = c / (D / 4), ch = c % (D / 4);
-                *reinterpret_cast<f32x4_t*>(Ks + key * C::ROWF + 4 * ch) = rk[i];
-                *reinterpret_cast<f32x4_t*>(Vs + key * C::ROWF + 4 * ch) = rv[i];
-            }
+        for (int i = 0; i < C::PT; ++i) {
+            const int c = lane + 64 * i;
+            const int key = c / (D / 4), ch = c % (D / 4);
+            *reinterpret_cast<f32x4_t*>(Ks + key * C::ROWF + 4 * ch) = rk[i];
+            *reinterpret_cast<f32x4_t*>(Vs + key * C::ROWF + 4 * ch) = rv[i];
         }
     };
 
@@ -615,17 +629,14 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_f32(
         for (int e = 0; e < 16; ++e) acc_o[i][e] = 0.0f;
     float m_run = kNegInf, l_run = 0.0f;
 
-    auto compute = [&](int stage, int k0) {
-        if (CAUSAL && k0 > qw0 + 31) return;
-        const float* Ks = smem + stage * C::STAGE_FLOATS;
-        const float* Vs = Ks + C::K_FLOATS;
+    auto compute = [&](int k0) {
         f32x16_t s;
 #pragma unroll
         for (int e = 0; e < 16; ++e) s[e] = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < D / 2; ++ks)
             s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[col * C::ROWF + 2 * ks + g], qf[ks], s, 0, 0, 0);
-        const bool need_mask = (k0 + BKV > S) || (CAUSAL && k0 + BKV - 1 > qw0);
+        const bool need_mask = (k0 + BKV > S) || (CAUSAL && k0 + BKV - 1 > q0);
         if (need_mask) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -665,45 +676,88 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_f32(
             }
     };
 
-    if (n_kv > 0) {
-        gload(0);
-        lstore(0);
-        __syncthreads();
-        for (int j = 0; j < n_kv; ++j) {
-            const bool more = j + 1 < n_kv;
-            if (more) gload((j + 1) * BKV);
-            compute(j & 1, j * BKV);
-            if (more) lstore((j + 1) & 1);
-            __syncthreads();
+    // this wave's key tiles: wave, wave + 4, ...
+    if (wave < n_kv) {
+        gload(wave * BKV);
+        lstore();
+        for (int j = wave; j < n_kv; j += NWF) {
+            const bool more = j + NWF < n_kv;
+            if (more) gload((j + NWF) * BKV);
+            compute(j * BKV);
+            if (more) lstore();
         }
     }
 
-    const float l_tot = l_run + xor32(l_run);
-    const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-    if (qrow < S) {
-        float* Orow = O + hoff + (int64_t)qrow * D;
+    // ---- merge the four partial states: M = max m_w, O = sum acc_w 2^(m_w - M),
+    // L = sum l_w 2^(m_w - M), in wave order ----
+    __syncthreads();  // every wave is done with its K/V tile
+    float* macc = smem + wave * (BQF * D + 2 * BQF);  // [q][d] accumulator, then m[q], l[q]
+    const float l_pair = l_run + xor32(l_run);
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+    for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-                f32x4_t w;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) w[i] = acc_o[dt][4 * jb + i] * inv;
-                *reinterpret_cast<f32x4_t*>(Orow + dt * 32 + 8 * jb + 4 * g) = w;
-            }
-        if (lse && g == 0)
-            lse[(int64_t)bh * S + qrow] = (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f;
+        for (int e = 0; e < 16; ++e) {
+            const int d = dt * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+            macc[col * D + d] = acc_o[dt][e];
+        }
+    if (g == 0) {
+        macc[BQF * D + col] = m_run;
+        macc[BQF * D + BQF + col] = l_pair;
     }
+    __syncthreads();
+    // every wave merges D/4 of the d columns of all 32 queries: lane -> (q, 8 d)
+    const int q = lane >> 1;
+    const int dbase = wave * (D / 4) + (lane & 1) * (D / 8);
+    float mw[NWF], mm = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NWF; ++w) {
+        mw[w] = smem[w * (BQF * D + 2 * BQF) + BQF * D + q];
+        mm = fmaxf(mm, mw[w]);
+    }
+    const float m_ref = (mm == kNegInf) ? 0.0f : mm;
+    float sc[NWF], L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWF; ++w) {
+        sc[w] = (mw[w] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - m_ref);
+        L += smem[w * (BQF * D + 2 * BQF) + BQF * D + BQF + q] * sc[w];
+    }
+    const float inv = (L > 0.0f) ? 1.0f / L : 0.0f;
+    const int orow = q0 + q;
+    if (orow < S) {
+        float* Orow = O + hoff + (int64_t)orow * D;
+#pragma unroll
+        for (int c4 = 0; c4 < D / 32; ++c4) {
+            f32x4_t v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = dbase + 4 * c4 + i;
+                float o = 0.0f;
+#pragma unroll
+                for (int w = 0; w < NWF; ++w) o += smem[w * (BQF * D + 2 * BQF) + q * D + d] * sc[w];
+                v[i] = o * inv;
+            }
+            *reinterpret_cast<f32x4_t*>(Orow + dbase + 4 * c4) = v;
+        }
+        if (lse && wave == 0 && (lane & 1) == 0)
+            lse[(int64_t)bh * S + orow] = (mm + __builtin_amdgcn_logf(L)) * 0.6931471805599453f;
+    }
+}
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void flash_fwd_f32(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ lse, int BH, int S, float c_log2) {
+    flash_f32_body<D, CAUSAL>(Q, K, V, O, lse, BH, S, c_log2);
 }
 
 template <typename KFN, typename T>
 hipError_t go(KFN kfn, const void* Q, const void* K, const void* V, void* O, float* lse, int BH,
               int S, float c_log2, hipStream_t s) {
-    // bf16: 256-row blocks of 8 waves; fp32: 128-row blocks of 4 waves
+    // bf16: 256-row blocks of 8 waves; fp32: 32-row blocks of 4 waves
     constexpr bool BF = sizeof(T) == 2;
-    const int bq = BF ? BQ2 : BQ;
+    const int bq = BF ? BQ2 : BQF;
     const int nq = (S + bq - 1) / bq;
-    hipLaunchKernelGGL(kfn, dim3(BH * nq), dim3((BF ? NW2 : NW) * 64), 0, s, static_cast<const T*>(Q),
+    hipLaunchKernelGGL(kfn, dim3(BH * nq), dim3((BF ? NW2 : NWF) * 64), 0, s, static_cast<const T*>(Q),
                        static_cast<const T*>(K), static_cast<const T*>(V), static_cast<T*>(O), lse,
                        BH, S, c_log2);
     return hipGetLastError();
@@ -715,7 +769,7 @@ hipError_t launch_flash_fwd(int dtype, int causal, float scale, const void* Q, c
                             const void* V, void* O, float* lse, int B, int H, int S, int D,
                             hipStream_t s) {
     const int BH = B * H;
-    if ((int64_t)BH * ((S + BQ - 1) / BQ) > 2147483647) return hipErrorInvalidValue;
+    if ((int64_t)BH * ((S + BQF - 1) / BQF) > 2147483647) return hipErrorInvalidValue;
     const float c = scale * kLog2e;
     if (dtype == JH_BF16) {
         if (D == 128)
