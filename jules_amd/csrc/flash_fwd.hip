@@ -596,18 +596,16 @@ __device__ __forceinline__ void flash_f32_body(
     float* Ks = smem + wave * C::WAVE_FLOATS;  // this wave's tile
     float* Vs = Ks + C::K_FLOATS;
     f32x4_t rk[C::PT], rv[C::PT];
+    // rows past S read row S-1 (branch-free loads): their scores are masked
+    // to -inf, so their p is 0 and the values never reach the output
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < C::PT; ++i) {
             const int c = lane + 64 * i;
             const int key = c / (D / 4), ch = c % (D / 4);
-            f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-            if (k0 + key < S) {
-                a = *reinterpret_cast<const f32x4_t*>(Kh + (int64_t)(k0 + key) * D + 4 * ch);
-                b = *reinterpret_cast<const f32x4_t*>(Vh + (int64_t)(k0 + key) * D + 4 * ch);
-            }
-            rk[i] = a;
-            rv[i] = b;
+            const int64_t row = min(k0 + key, S - 1);
+            rk[i] = *reinterpret_cast<const f32x4_t*>(Kh + row * D + 4 * ch);
+            rv[i] = *reinterpret_cast<const f32x4_t*>(Vh + row * D + 4 * ch);
         }
     };
     // the wave's LDS reads of the previous tile are issued before these
@@ -630,12 +628,17 @@ __device__ __forceinline__ void flash_f32_body(
     float m_run = kNegInf, l_run = 0.0f;
 
     auto compute = [&](int k0) {
-        f32x16_t s;
+        // two independent accumulation chains (even / odd k-steps), summed
+        f32x16_t s, s1;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+        for (int e = 0; e < 16; ++e) s[e] = s1[e] = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < D / 2; ++ks)
+        for (int ks = 0; ks < D / 2; ks += 2) {
             s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[col * C::ROWF + 2 * ks + g], qf[ks], s, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[col * C::ROWF + 2 * ks + 2 + g], qf[ks + 1],
+                                                      s1, 0, 0, 0);
+        }
+        s += s1;
         const bool need_mask = (k0 + BKV > S) || (CAUSAL && k0 + BKV - 1 > q0);
         if (need_mask) {
 #pragma unroll
