@@ -170,6 +170,27 @@ class Runner:
         return self.work / (ms * 1e-3) / 1e12 if self.unit == "TFLOP/s" else self.work / (ms * 1e-3) / 1e9
 
 
+class CeilingRunner:
+    """The MFMA calibration kernel (jules_hip_mfma_ceiling): one workgroup per
+    CU issuing independent bf16 MFMAs on random operands, ~1 ms per launch.
+    Its rate is the MFMA rate the part sustains under load (the engine clock
+    drops under the power limit), the clock-adjusted peak reported next to
+    PEAK["bf16"]."""
+
+    name = "mfma_ceiling"
+
+    def __init__(self, dev, iters=3072):
+        import torch
+        self.wg = torch.cuda.get_device_properties(dev).multi_processor_count
+        self.iters = iters
+        self.out = torch.empty(self.wg * 256, dtype=torch.float32, device=dev)
+        self.work = 32768.0 * 16 * iters * 4 * self.wg
+
+    def launch(self):
+        from jules_amd import ops
+        ops.mfma_ceiling(self.out, self.wg, self.iters)
+
+
 def time_launches(runners, warmup, iters):
     """Run `iters` rounds of launching every runner once, with a HIP event pair
     around each launch on the stream the kernels run on (torch's current
@@ -281,11 +302,13 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-calib", action="store_true", help="skip the MFMA ceiling calibration")
     ap.add_argument("--only", default="", help="comma list of per-config runs (default all)")
     ap.add_argument("--step-only", action="store_true", help="skip the per-config runs")
     ap.add_argument("--pmc", action="store_true",
                     help="counter-collection workload for rocprofv3 --pmc: one 64 MiB device "
-                         "copy of known size (calibration), then 3 launches of C3, C4 and C5")
+                         "copy of known size (calibration), 3 MFMA calibration launches, then 3 "
+                         "launches of C3, C4 and C5")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -301,6 +324,11 @@ def main():
         dst = torch.empty_like(src)
         dst.copy_(src)  # 64 MiB read + 64 MiB write: the calibration dispatch
         torch.cuda.synchronize()
+        c = CeilingRunner(dev)
+        for _ in range(3):
+            c.launch()  # MFMA calibration dispatches (clock and MFMA busy under load)
+        torch.cuda.synchronize()
+        del c
         for name in ("c3", "c4", "c5"):
             r = Runner(name, CONFIGS[name], dev)
             for _ in range(3):
@@ -352,6 +380,24 @@ def main():
     del step
     torch.cuda.empty_cache()
 
+    # ---- clock-adjusted MFMA peak: the calibration kernel's sustained rate ----
+    ceiling = None
+    if not args.no_calib:
+        log("mfma ceiling")
+        try:
+            c = CeilingRunner(dev)
+            cd, _ = time_launches([c], 3, 10)
+            cmed = statistics.median(cd[0])
+            crate = c.work / (cmed * 1e-3) / 1e12
+            ceiling = {"value": crate, "unit": "TFLOP/s", "kernel": "mfma_ceiling_kernel",
+                       "median_ms": cmed, "frac_of_peak": crate / PEAK["bf16"],
+                       "headline_frac": value / crate,
+                       "dominant_kernel_frac": (roofline["achieved"] / crate
+                                                if roofline["unit"] == "TFLOP/s" else None)}
+            del c
+        except Exception as e:
+            ceiling = {"error": f"{type(e).__name__}: {e}"}
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -377,6 +423,7 @@ def main():
                                "fwd [B8,H32,S4096,D128]",
                    "flop_per_step": work, "step_kernels": step_kernels},
         "roofline": roofline,
+        "mfma_ceiling": ceiling,
         "cpu_baseline": cpu,
         "per_config": per,
         "device": torch.cuda.get_device_name(0),

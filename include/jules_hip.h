@@ -203,6 +203,18 @@ int jules_hip_cross_entropy(const float* logits, const int32_t* targets,
                             void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* ---- MFMA calibration -----------------------------------------------------
+ * No counterpart in the reference: a roofline calibration for callers that
+ * report MFMA rates against the rate the part sustains under load (its engine
+ * clock drops under the power limit when the matrix cores are busy).  Launches
+ * `workgroups` x 4 waves; each wave issues 16 * iters independent
+ * v_mfma_f32_32x32x16_bf16 on random bf16 operands held in registers, i.e.
+ * 32768 * 16 * iters * 4 * workgroups FLOP in total.  out: device fp32
+ * [workgroups * 256], 4-byte aligned; its values only keep the work live.
+ * workgroups in [1, 65535], iters in [1, 1 << 20].
+ */
+int jules_hip_mfma_ceiling(float* out, int workgroups, int iters, void* stream);
+
 /* ---- kernel-name registry -------------------------------------------------
  * Resolves the names KernelRoutingPass emits (fusedMatmul{Relu,Sigmoid,Tanh,
  * Gelu}, fusedMatmulBias{Relu,Sigmoid,Tanh,Gelu}, fusedGelu, matmulInt8,

@@ -45,6 +45,7 @@ SIGNATURES = {
                                              _vp, _size, _vp]),
     "jules_hip_matmul_int8": (_int, [_vp, _vp, _vp, _int, _int, _int, _f32, _f32, _vp, _vp]),
     "jules_hip_softmax": (_int, [_vp, _vp, _int, _int, _vp]),
+    "jules_hip_mfma_ceiling": (_int, [_vp, _int, _int, _vp]),
     "jules_hip_layernorm": (_int, [_vp, _vp, _vp, _vp, _int, _int, _f32, _vp]),
     "jules_hip_cross_entropy_workspace_size": (_size, [_int]),
     "jules_hip_cross_entropy": (_int, [_vp, _vp, _vp, _vp, _int, _int, _vp, _size, _vp]),

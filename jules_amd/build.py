@@ -26,7 +26,7 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
           "-munsafe-fp-atomics"]
 
 SOURCES = ["gemm_f32.hip", "gemm_bf16.hip", "flash_fwd.hip", "w8a16.hip", "matmul_int8.hip",
-           "rowops.hip", "capi.cpp", "kernel_shims.cpp"]
+           "rowops.hip", "calib.hip", "capi.cpp", "kernel_shims.cpp"]
 
 
 def _compile(src, verbose):

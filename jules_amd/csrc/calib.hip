@@ -1,0 +1,80 @@
+// calib.hip - MFMA rate calibration for the roofline (no counterpart in the
+// reference).
+//
+// A stream of independent v_mfma_f32_32x32x16_bf16 on random bf16 operands
+// held in registers.  It measures the MFMA rate the part sustains under load:
+// the engine clock drops under the power limit as MFMA activity rises
+// (measured: ~93% MFMA busy at ~1.7 GHz instead of 2.4 GHz), so this is the
+// clock-adjusted peak that the hot-path kernels' MFMA rates are compared with,
+// next to the published 2516.6 TFLOP/s.  Operands come from a hash of
+// (wave, lane, index), uniform in [-1, 1) at bf16 precision, so the
+// multipliers toggle like they do on real data (all-zero operands run faster).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace jh {
+namespace {
+
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352dU;
+    x ^= x >> 15;
+    x *= 0x846ca68bU;
+    x ^= x >> 16;
+    return x;
+}
+
+// 4 waves, 16 MFMAs per iteration into 8 accumulators (two uses each, never
+// back to back)
+__global__ __launch_bounds__(256, 1) void mfma_ceiling_kernel(float* __restrict__ out, int iters) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    bf16x8_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u32x4_t ua, ub;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t h0 = mix32((wid * 64 + lane) * 32 + i * 8 + 2 * w);
+            const uint32_t h1 = mix32((wid * 64 + lane) * 32 + i * 8 + 2 * w + 1);
+            const float s = 1.0f / 32768.0f;
+            ua[w] = pack_bf16x2((float)(h0 & 0xffff) * s - 1.0f, (float)(h1 & 0xffff) * s - 1.0f);
+            ub[w] = pack_bf16x2((float)(h0 >> 16) * s - 1.0f, (float)(h1 >> 16) * s - 1.0f);
+        }
+        a[i] = __builtin_bit_cast(bf16x8_t, ua);
+        b[i] = __builtin_bit_cast(bf16x8_t, ub);
+    }
+    f32x16_t acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2 * r + i], b[j], acc[i][j], 0, 0, 0);
+    }
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t += acc[i][j][e];
+    out[(int64_t)blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+}  // namespace
+
+hipError_t launch_mfma_ceiling(float* out, int workgroups, int iters, hipStream_t s) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(workgroups), dim3(256), 0, s, out, iters);
+    return hipGetLastError();
+}
+
+}  // namespace jh

@@ -204,6 +204,16 @@ int jules_hip_layernorm(float* out, const float* in, const float* gamma, const f
                      "layernorm launch");
 }
 
+int jules_hip_mfma_ceiling(float* out, int workgroups, int iters, void* stream) {
+    if (!out) return fail(JH_ERR_NULL, "mfma_ceiling: null out");
+    if (!aligned(out, 4)) return fail(JH_ERR_ALIGN, "mfma_ceiling: out must be 4-byte aligned");
+    if (workgroups < 1 || workgroups > 65535 || iters < 1 || iters > (1 << 20))
+        return fail(JH_ERR_SHAPE, "mfma_ceiling: workgroups %d (1..65535), iters %d (1..1048576)",
+                    workgroups, iters);
+    return check_hip(jh::launch_mfma_ceiling(out, workgroups, iters, static_cast<hipStream_t>(stream)),
+                     "mfma_ceiling");
+}
+
 size_t jules_hip_cross_entropy_workspace_size(int M) {
     return M > 0 ? (size_t)M * sizeof(float) : sizeof(float);
 }

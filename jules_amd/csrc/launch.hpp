@@ -29,4 +29,7 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
 hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, float* grad,
                                 float* loss, float* row_loss, int M, int N, hipStream_t s);
 
+// calibration: workgroups x 4 waves x 16*iters MFMAs on random operands
+hipError_t launch_mfma_ceiling(float* out, int workgroups, int iters, hipStream_t s);
+
 }  // namespace jh

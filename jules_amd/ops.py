@@ -189,3 +189,16 @@ def cross_entropy(logits, targets, grad=None, loss=None, workspace=None):
     check(lib().jules_hip_cross_entropy(_ptr(logits), _ptr(targets), _ptr(grad), _ptr(loss), M, N,
                                         _ptr(workspace), workspace.numel() * 4, _stream(logits)))
     return loss, grad
+
+
+def mfma_ceiling(out, workgroups, iters):
+    """Launch the MFMA calibration kernel (jules_hip_mfma_ceiling; no
+    counterpart in the reference) on torch's current stream: `workgroups` x 4
+    waves, each issuing 16 * iters v_mfma_f32_32x32x16_bf16 on random
+    operands.  out: fp32 GPU tensor of workgroups * 256 elements.  Returns
+    the FLOP count of the launch."""
+    _need(out, "out", (torch.float32,))
+    if out.numel() < workgroups * 256:
+        raise ValueError("out must hold workgroups * 256 floats")
+    check(lib().jules_hip_mfma_ceiling(_ptr(out), int(workgroups), int(iters), _stream(out)))
+    return 32768.0 * 16 * iters * 4 * workgroups

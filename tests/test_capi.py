@@ -177,3 +177,14 @@ def test_rowops_validation():
     assert L.jules_hip_cross_entropy(None, None, None, None, 3, 5, None, 0, None) == 1
     assert L.jules_hip_cross_entropy(16, 16, 16, 16, 3, 5, None, 0, None) == 6   # workspace
     assert L.jules_hip_cross_entropy(16, 16, 16, 16, 3, 5, 16, 8, None) == 6
+
+
+def test_mfma_ceiling_validation():
+    """The calibration entry point rejects bad arguments before any launch."""
+    L = _lib.lib()
+    assert L.jules_hip_mfma_ceiling(None, 4, 16, None) == 1            # null
+    assert L.jules_hip_mfma_ceiling(2, 4, 16, None) == 4               # misaligned
+    assert L.jules_hip_mfma_ceiling(16, 0, 16, None) == 2              # no workgroups
+    assert L.jules_hip_mfma_ceiling(16, 65536, 16, None) == 2
+    assert L.jules_hip_mfma_ceiling(16, 4, 0, None) == 2               # no iterations
+    assert L.jules_hip_mfma_ceiling(16, 4, (1 << 20) + 1, None) == 2
