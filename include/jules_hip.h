@@ -254,6 +254,32 @@ jh_kernel_fn jules_hip_lookup(const char* name);
 int jules_hip_kernel_count(void);
 const char* jules_hip_kernel_name(int index);
 
+/* ---- ROCm PJRT executor ----------------------------------------------------
+ * C access to the ROCm PJRT client of jules_hip_pjrt.hpp, whose classes
+ * mirror the reference's PJRTClient / PJRTDevice / PJRTExecutable
+ * (include/jules/PJRT.h:113-233).  A program is StableHLO text in generic op
+ * form, read with the reference CPU executable's parse rules and op semantics
+ * (lib/PJRT.cpp:169-858); stablehlo.custom_call runs the registry kernel its
+ * call_target_name names instead of the reference's copy (PJRT.cpp:491-499).
+ *
+ * jules_hip_pjrt_compile: loads `program` onto GPU `device`; *exe receives a
+ *   handle for execute/destroy.
+ * jules_hip_pjrt_execute: runs the program on the inputs (contiguous device
+ *   tensors, not modified) and returns after the GPU is done.  outputs[0..)
+ *   receive descriptors of every value the program produced, in program
+ *   order (*n_outputs of them; JH_ERR_WORKSPACE when more than max_outputs).
+ *   Their memory belongs to the handle and stays valid until the next execute
+ *   on it or its destruction.
+ * jules_hip_pjrt_describe: the parsed op list for n_inputs inputs as text
+ *   (needs no GPU); JH_ERR_WORKSPACE if buf_len is too small.
+ */
+typedef struct jh_pjrt_exe jh_pjrt_exe;
+int jules_hip_pjrt_compile(const char* program, int device, jh_pjrt_exe** exe);
+int jules_hip_pjrt_execute(jh_pjrt_exe* exe, int n_inputs, const jh_tensor* inputs,
+                           int max_outputs, jh_tensor* outputs, int* n_outputs);
+int jules_hip_pjrt_destroy(jh_pjrt_exe* exe);
+int jules_hip_pjrt_describe(const char* program, int n_inputs, char* buf, size_t buf_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,11 @@ SIGNATURES = {
     "jules_hip_lookup": (_vp, [ctypes.c_char_p]),
     "jules_hip_kernel_count": (_int, []),
     "jules_hip_kernel_name": (ctypes.c_char_p, [_int]),
+    "jules_hip_pjrt_compile": (_int, [ctypes.c_char_p, _int, ctypes.POINTER(_vp)]),
+    "jules_hip_pjrt_execute": (_int, [_vp, _int, ctypes.POINTER(JhTensor), _int,
+                                      ctypes.POINTER(JhTensor), ctypes.POINTER(_int)]),
+    "jules_hip_pjrt_destroy": (_int, [_vp]),
+    "jules_hip_pjrt_describe": (_int, [ctypes.c_char_p, _int, ctypes.c_char_p, _size]),
 }
 
 _lib = None

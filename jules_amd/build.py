@@ -26,7 +26,8 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
           "-munsafe-fp-atomics"]
 
 SOURCES = ["gemm_f32.hip", "gemm_bf16.hip", "flash_fwd.hip", "w8a16.hip", "matmul_int8.hip",
-           "rowops.hip", "calib.hip", "capi.cpp", "kernel_shims.cpp"]
+           "rowops.hip", "calib.hip", "pjrt_ops.hip", "capi.cpp", "kernel_shims.cpp",
+           "pjrt.cpp"]
 
 
 def _compile(src, verbose):
@@ -57,7 +58,23 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    _build_selftests(verbose)
     return LIB
+
+
+def _build_selftests(verbose):
+    """Host-only C++ test programs linked against the library (g++)."""
+    src = os.path.join(ROOT, "tests", "cpp", "pjrt_selftest.cpp")
+    if not os.path.exists(src):
+        return
+    out = os.path.join(ROOT, "tests", "cpp", "pjrt_selftest")
+    cmd = ["g++", "-O2", "-std=c++17", f"-I{INCLUDE}", src, f"-L{HERE}", "-ljules_hip",
+           "-Wl,-rpath,$ORIGIN/../../jules_amd", "-o", out]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on {src}:\n{r.stdout}\n{r.stderr}")
 
 
 if __name__ == "__main__":

@@ -48,6 +48,15 @@ constexpr int64_t kMaxElems = int64_t(1) << 40;
 
 }  // namespace
 
+namespace jh {
+// Lets other translation units of the library (pjrt.cpp) report through
+// jules_hip_last_error().
+int set_last_error(int status, const std::string& message) {
+    g_last_error = message;
+    return status;
+}
+}  // namespace jh
+
 extern "C" {
 
 int jules_hip_abi_version(void) { return JULES_HIP_ABI_VERSION; }

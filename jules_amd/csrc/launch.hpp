@@ -29,6 +29,24 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
 hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, float* grad,
                                 float* loss, float* row_loss, int M, int N, hipStream_t s);
 
+// PJRT executor ops (pjrt_ops.hip): fp32, rank <= 8
+enum PjOp {
+    PJ_ADD = 0, PJ_SUB, PJ_MUL, PJ_DIV, PJ_MAX, PJ_MIN,
+    PJ_NEG, PJ_RELU, PJ_SIGMOID, PJ_TANH, PJ_EXP, PJ_LOG
+};
+struct PjIndexMap {
+    int rank;
+    int64_t out_stride[8];  // strides of the index space walked
+    int64_t in_step[8];     // input offset per unit step of each index
+};
+hipError_t launch_pj_binary(int op, const float* a, int64_t na, const float* b, int64_t nb,
+                            float* out, int64_t n, hipStream_t s);
+hipError_t launch_pj_unary(int op, const float* a, float* out, int64_t n, hipStream_t s);
+hipError_t launch_pj_transpose(const float* in, float* out, int64_t n, const PjIndexMap& map,
+                               hipStream_t s);
+hipError_t launch_pj_reduce(const float* in, float* out, int64_t n_out, int64_t n_red,
+                            const PjIndexMap& keep, const PjIndexMap& red, hipStream_t s);
+
 // calibration: workgroups x 4 waves x 16*iters MFMAs on random operands
 hipError_t launch_mfma_ceiling(float* out, int workgroups, int iters, hipStream_t s);
 
