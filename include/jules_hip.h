@@ -164,6 +164,21 @@ int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M,
                           int N, int K, float scale_A, float scale_B,
                           const float* bias, void* stream);
 
+/* ---- W8A8 GEMM with per-token / per-channel scales ---------------------------
+ * C[i,j] = float(sum_k A[i,k]*B[k,j]) * (sA_i * sB_j) [+ bias[j]]
+ * The matmulInt8 the routing pass would emit once QuantizePass carries
+ * scales (the reference's matmulInt8, FusedKernels.h:867-1073, has
+ * per-tensor scales only): B indexed B[k*N+j]
+ * like the scalar path, exact int32 accumulation, the scale product
+ * sA_i * sB_j rounded to fp32 per element, one multiply, one add of bias.
+ * With constant scale vectors the result equals jules_hip_matmul_int8 bit for
+ * bit.  scale_A: fp32 [M] per-token scales, or NULL for 1; scale_B: fp32 [N]
+ * per-output-channel scales (required).  K <= 131072.
+ */
+int jules_hip_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M,
+                          int N, int K, const float* scale_A,
+                          const float* scale_B, const float* bias, void* stream);
+
 /* ---- row kernels ----------------------------------------------------------
  * fp32, row-major [M, N], device pointers, 4-byte aligned; out may alias in.
  * Each row is processed with the reference's per-element arithmetic (exp
@@ -221,13 +236,14 @@ int jules_hip_mfma_ceiling(float* out, int workgroups, int iters, void* stream);
  * flashAttention, fusedSoftmax, fusedLayerNorm, fusedCrossEntropyLoss) and
  * the ones this library adds (fusedMatmul,
  * fusedMatmulBias, fusedMatmulBiasSilu, flashAttentionCausal,
- * matmulW8A16BiasSilu) to a descriptor-based entry point.  The descriptor
+ * matmulW8A16BiasSilu, matmulW8A8) to a descriptor-based entry point.  The descriptor
  * extends the reference's TensorDescriptor (include/jules/LLVMBackend.h:60-66:
  * data, offset, sizes[6], strides[6], rank) with a dtype; data + offset is
  * the device address of element 0 and strides are in elements.
  * Operand order follows extern_kernel: (lhs, rhs[, bias]) for the matmuls
  * (KernelRoutingPass.cpp:154,198), (Q, K, V) for attention,
- * (x, W, scale[, bias]) for W8A16, (A, B[, bias]) plus backend_config
+ * (x, W, scale[, bias]) for W8A16, (A, B, scale_A, scale_B[, bias]) for
+ * matmulW8A8, (A, B[, bias]) plus backend_config
  * "scale_a=<f>,scale_b=<f>" for matmulInt8 (the reference emits no scales,
  * KernelRoutingPass.cpp:406-410).  Attention accepts backend_config
  * "scale=<f>"; the default is 1/sqrtf(D).  Row kernels: (x) -> y for

@@ -44,6 +44,7 @@ SIGNATURES = {
     "jules_hip_w8a16_gemm_bias_act": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _int, _int, _int,
                                              _vp, _size, _vp]),
     "jules_hip_matmul_int8": (_int, [_vp, _vp, _vp, _int, _int, _int, _f32, _f32, _vp, _vp]),
+    "jules_hip_matmul_w8a8": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp, _vp, _vp, _vp]),
     "jules_hip_softmax": (_int, [_vp, _vp, _int, _int, _vp]),
     "jules_hip_mfma_ceiling": (_int, [_vp, _int, _int, _vp]),
     "jules_hip_layernorm": (_int, [_vp, _vp, _vp, _vp, _int, _int, _f32, _vp]),

@@ -181,6 +181,23 @@ int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int
                      "matmulInt8 launch");
 }
 
+int jules_hip_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
+                          const float* scale_A, const float* scale_B, const float* bias,
+                          void* stream) {
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "matmulW8A8: M=%d N=%d K=%d", M, N, K);
+    if (K > 131072) return fail(JH_ERR_SHAPE, "matmulW8A8: K=%d exceeds exact int32 range", K);
+    if ((int64_t)M * K > kMaxElems || (int64_t)K * N > kMaxElems || (int64_t)M * N > kMaxElems)
+        return fail(JH_ERR_SHAPE, "matmulW8A8: too large");
+    if (M == 0 || N == 0) return JH_OK;
+    if (!C || !scale_B || (K > 0 && (!A || !B)))
+        return fail(JH_ERR_NULL, "matmulW8A8: null A, B, C or scale_B");
+    if (!aligned(C, 4) || !aligned(bias, 4) || !aligned(scale_A, 4) || !aligned(scale_B, 4))
+        return fail(JH_ERR_ALIGN, "matmulW8A8: alignment");
+    return check_hip(jh::launch_matmul_w8a8(A, B, C, M, N, K, scale_A, scale_B, bias,
+                                            static_cast<hipStream_t>(stream)),
+                     "matmulW8A8 launch");
+}
+
 // Row kernels (reference FusedKernels.h:464-526, :532-600, :766-854).
 static int row_shape(const char* who, int M, int N) {
     if (M < 0 || N < 0) return fail(JH_ERR_SHAPE, "%s: M=%d N=%d", who, M, N);
@@ -457,6 +474,34 @@ int k_int8(int ni, const jh_tensor* in, int no, jh_tensor* out, const char* cfg,
                                  bias, s);
 }
 
+int k_w8a8(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
+    if ((ni != 4 && ni != 5) || no != 1 || !in || !out)
+        return fail(JH_ERR_ARG, "matmulW8A8: (A, B, scale_A, scale_B[, bias]) -> C");
+    const jh_tensor &a = in[0], &b = in[1], &sa = in[2], &sb = in[3];
+    jh_tensor& c = out[0];
+    if (a.rank != 2 || b.rank != 2 || c.rank != 2 || !contiguous(a) || !contiguous(b) ||
+        !contiguous(c))
+        return fail(JH_ERR_SHAPE, "matmulW8A8: 2-D contiguous A, B, C");
+    if (a.dtype != JH_I8 || b.dtype != JH_I8 || c.dtype != JH_F32 || sa.dtype != JH_F32 ||
+        sb.dtype != JH_F32)
+        return fail(JH_ERR_DTYPE, "matmulW8A8: int8 x int8 -> fp32, fp32 scales");
+    const int64_t M = a.sizes[0], K = a.sizes[1], N = b.sizes[1];
+    if (b.sizes[0] != K || c.sizes[0] != M || c.sizes[1] != N)
+        return fail(JH_ERR_SHAPE, "matmulW8A8: shape mismatch");
+    if (numel(sa) != M || numel(sb) != N || !contiguous(sa) || !contiguous(sb))
+        return fail(JH_ERR_SHAPE, "matmulW8A8: scale_A [M], scale_B [N]");
+    const float* bias = nullptr;
+    if (ni == 5) {
+        if (in[4].dtype != JH_F32 || numel(in[4]) != N || !contiguous(in[4]))
+            return fail(JH_ERR_SHAPE, "matmulW8A8: bias fp32 [N]");
+        bias = static_cast<const float*>(addr(in[4]));
+    }
+    return jules_hip_matmul_w8a8(static_cast<const int8_t*>(addr(a)), static_cast<const int8_t*>(addr(b)),
+                                 static_cast<float*>(addr_mut(c)), (int)M, (int)N, (int)K,
+                                 static_cast<const float*>(addr(sa)), static_cast<const float*>(addr(sb)),
+                                 bias, s);
+}
+
 // rows of a descriptor: product of all but the last dimension
 int64_t rows_of(const jh_tensor& t) {
     int64_t r = 1;
@@ -549,6 +594,7 @@ const Entry kRegistry[] = {
     {"fusedMatmulBiasSilu", k_matmul_bias_silu},
     {"flashAttentionCausal", k_attn_causal},
     {"matmulW8A16BiasSilu", k_w8a16_silu},
+    {"matmulW8A8", k_w8a8},
 };
 constexpr int kRegistrySize = sizeof(kRegistry) / sizeof(kRegistry[0]);
 

@@ -22,6 +22,9 @@ hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float
                         hipStream_t s);
 hipError_t launch_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                               float scale_a, float scale_b, const float* bias, hipStream_t s);
+hipError_t launch_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
+                              const float* scale_a, const float* scale_b, const float* bias,
+                              hipStream_t s);
 hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t s);
 hipError_t launch_layernorm(float* out, const float* in, const float* gamma, const float* beta,
                             int M, int N, float eps, hipStream_t s);

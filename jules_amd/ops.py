@@ -202,3 +202,30 @@ def mfma_ceiling(out, workgroups, iters):
         raise ValueError("out must hold workgroups * 256 floats")
     check(lib().jules_hip_mfma_ceiling(_ptr(out), int(workgroups), int(iters), _stream(out)))
     return 32768.0 * 16 * iters * 4 * workgroups
+
+
+
+def matmul_w8a8(A, B, scale_a, scale_b, bias=None, out=None):
+    """C = float(A @ B) * (scale_a[i] * scale_b[j]) [+ bias] with exact int32
+    accumulation (jules_hip_matmul_w8a8): int8 A [M,K], B [K,N], fp32
+    per-token scale_a [M] (or None) and per-channel scale_b [N]."""
+    _need(A, "A", (torch.int8,))
+    _need(B, "B", (torch.int8,), A.device)
+    M, K = A.shape
+    K2, N = B.shape
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    if scale_a is not None:
+        _need(scale_a, "scale_a", (torch.float32,), A.device)
+        if scale_a.numel() != M:
+            raise ValueError("scale_a must have M elements")
+    _need(scale_b, "scale_b", (torch.float32,), A.device)
+    if scale_b.numel() != N:
+        raise ValueError("scale_b must have N elements")
+    if bias is not None:
+        _need(bias, "bias", (torch.float32,), A.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=A.device)
+    check(lib().jules_hip_matmul_w8a8(_ptr(A), _ptr(B), _ptr(out), M, N, K, _ptr(scale_a),
+                                      _ptr(scale_b), _ptr(bias), _stream(A)))
+    return out

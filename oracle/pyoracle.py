@@ -224,6 +224,25 @@ def matmul_int8(A, B, scale_a, scale_b, bias=None):
     return out
 
 
+def w8a8(A, B, scale_a, scale_b, bias=None):
+    """W8A8 with per-token scales scale_a [M] (None: 1) and per-channel scales
+    scale_b [N]: the per-element form of matmulInt8's scalar path
+    (FusedKernels.h:1046-1066).  Exact integer accumulation, the product
+    scale_a[i] * scale_b[j] rounded to fp32, one fp32 multiply of the
+    fp32-rounded integer, one fp32 add of bias.  numpy, bit-exact."""
+    A = np.asarray(A, np.int8)
+    B = np.asarray(B, np.int8)
+    M, N = A.shape[0], B.shape[1]
+    acc = A.astype(np.int64) @ B.astype(np.int64)
+    sa = np.ones(M, np.float32) if scale_a is None else np.asarray(scale_a, np.float32)
+    sb = np.asarray(scale_b, np.float32)
+    prod = (sa[:, None] * sb[None, :]).astype(np.float32)
+    c = acc.astype(np.float32) * prod
+    if bias is not None:
+        c = c + np.asarray(bias, np.float32)[None, :]
+    return c.astype(np.float32)
+
+
 def w8a16(x, W, scale, bias, act):
     x = _f32(x)
     W = np.ascontiguousarray(W, np.int8)

@@ -188,3 +188,14 @@ def test_mfma_ceiling_validation():
     assert L.jules_hip_mfma_ceiling(16, 65536, 16, None) == 2
     assert L.jules_hip_mfma_ceiling(16, 4, 0, None) == 2               # no iterations
     assert L.jules_hip_mfma_ceiling(16, 4, (1 << 20) + 1, None) == 2
+
+
+def test_w8a8_validation():
+    """matmulW8A8 rejects bad arguments before touching the device."""
+    L = _lib.lib()
+    assert L.jules_hip_matmul_w8a8(None, None, None, -1, 4, 4, None, None, None, None) == 2
+    assert L.jules_hip_matmul_w8a8(None, None, None, 4, 4, 131073, None, None, None, None) == 2
+    assert L.jules_hip_matmul_w8a8(None, None, None, 0, 4, 4, None, None, None, None) == 0
+    assert L.jules_hip_matmul_w8a8(16, 16, 16, 4, 4, 4, None, None, None, None) == 1   # scale_B
+    assert L.jules_hip_matmul_w8a8(16, 16, 16, 4, 4, 4, 2, 16, None, None) == 4        # scale_A
+    assert L.jules_hip_matmul_w8a8(16, 16, 18, 4, 4, 4, None, 16, None, None) == 4      # C

@@ -12,7 +12,7 @@ import torch
 from jules_amd import _lib, ops
 from oracle import inputs as I
 from oracle import pyoracle as po
-from tests.helpers import case, to_dev, to_np
+from tests.helpers import case, registry_call, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 ACTS = ["none", "relu", "sigmoid", "tanh", "gelu", "silu"]
@@ -143,3 +143,49 @@ def _fill(d, t):
         d.sizes[i] = t.shape[i]
         d.strides[i] = t.stride(i)
     d.dtype = {torch.float32: 0, torch.bfloat16: 1, torch.int8: 2}[t.dtype]
+
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (8, 8192, 1024), (37, 129, 300), (256, 96, 4096)])
+def test_w8a8_bit_exact(dev, M, N, K):
+    """Per-token / per-channel W8A8 (jules_hip_matmul_w8a8) against the numpy
+    restatement, bit for bit, with and without bias and per-token scales."""
+    case(f"w8a8 M={M} N={N} K={K}")
+    A = I.int8_uniform(5, 0, (M, K))
+    B = I.int8_uniform(5, 1, (K, N))
+    sa = I.uniform(5, 2, (M,), 1e-3, 1e-2)
+    sb = I.uniform(5, 3, (N,), 1e-3, 1e-2)
+    bias = I.uniform(5, 4, (N,), -0.1, 0.1)
+    tA, tB = to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev)
+    for use_sa in (True, False):
+        for b in (None, bias):
+            y = ops.matmul_w8a8(tA, tB, to_dev(sa, torch.float32, dev) if use_sa else None,
+                                to_dev(sb, torch.float32, dev),
+                                None if b is None else to_dev(b, torch.float32, dev))
+            np.testing.assert_array_equal(to_np(y), po.w8a8(A, B, sa if use_sa else None, sb, b))
+
+
+def test_w8a8_constant_scales_equal_matmul_int8(dev):
+    case("w8a8 with constant scales == matmulInt8")
+    A = I.int8_uniform(6, 0, (33, 200))
+    B = I.int8_uniform(6, 1, (200, 70))
+    tA, tB = to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev)
+    y1 = ops.matmul_w8a8(tA, tB, to_dev(np.full(33, 0.013, np.float32), torch.float32, dev),
+                         to_dev(np.full(70, 0.021, np.float32), torch.float32, dev))
+    y2 = ops.matmul_int8(tA, tB, 0.013, 0.021)
+    assert torch.equal(y1, y2)
+
+
+def test_w8a8_registry(dev):
+    case("registry matmulW8A8")
+    A = I.int8_uniform(7, 0, (16, 64))
+    B = I.int8_uniform(7, 1, (64, 48))
+    sa = I.uniform(7, 2, (16,), 1e-3, 1e-2)
+    sb = I.uniform(7, 3, (48,), 1e-3, 1e-2)
+    bias = I.uniform(7, 4, (48,), -0.1, 0.1)
+    c = torch.empty((16, 48), dtype=torch.float32, device=dev)
+    st = registry_call("matmulW8A8", [to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev),
+                                      to_dev(sa, torch.float32, dev), to_dev(sb, torch.float32, dev),
+                                      to_dev(bias, torch.float32, dev)], [c])
+    assert st == 0, _lib.lib().jules_hip_last_error()
+    np.testing.assert_array_equal(to_np(c), po.w8a8(A, B, sa, sb, bias))

@@ -263,6 +263,29 @@ def test_flash_tiling_invariance():
 
 
 # ---- int8 / W8A16 ------------------------------------------------------------
+def test_w8a8_oracle_pinned():
+    """The per-token / per-channel W8A8 restatement: with constant scale vectors
+    it is matmulInt8's scalar path bit for bit; a one-hot A selects row k of B
+    times its scales exactly; fp64 agrees to fp32 rounding."""
+    A = I.int8_uniform(3, 0, (9, 70))
+    B = I.int8_uniform(3, 1, (70, 33))
+    bias = I.uniform(3, 2, (33,), -0.1, 0.1)
+    y = po.w8a8(A, B, np.full(9, 0.013, np.float32), np.full(33, 0.021, np.float32), bias)
+    assert np.array_equal(y, po.matmul_int8(A, B, 0.013, 0.021, bias))
+    sa = I.uniform(3, 3, (9,), 1e-3, 1e-2)
+    sb = I.uniform(3, 4, (33,), 1e-3, 1e-2)
+    e = np.zeros((9, 70), np.int8)
+    e[np.arange(9), np.arange(9) * 7] = 1
+    y1 = po.w8a8(e, B, sa, sb)
+    for i in range(9):
+        want = B[7 * i].astype(np.float32) * (np.float32(sa[i]) * sb)
+        assert np.array_equal(y1[i], want.astype(np.float32))
+    y2 = po.w8a8(A, B, sa, sb, bias)
+    ref = (A.astype(np.float64) @ B) * (sa.astype(np.float64)[:, None] * sb[None, :]) + bias
+    assert I.rel_err(y2, ref) < 1e-6
+    assert np.array_equal(po.w8a8(A, B, None, sb), po.w8a8(A, B, np.ones(9, np.float32), sb))
+
+
 def test_matmul_int8_exact():
     A = I.int8_uniform(1, 0, (9, 70))
     B = I.int8_uniform(1, 1, (70, 33))
