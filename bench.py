@@ -36,7 +36,7 @@ PEAK = {"bf16": 2516.6, "f32": 157.3, "hbm": 8000.0}  # TFLOP/s, TFLOP/s, GB/s
 MEASURED_TRAFFIC = {
     "c3": 201.7e6 + 33.9e6,   # gemm_bf16_dma_kernel<GELU>
     "c4": 806.1e6 + 268.4e6,  # flash_fwd_bf16<128, causal>
-    "c5": 68.3e6 + 2.1e6 + 2.2e6 + 0.1e6,  # w8a16 partial + finalize
+    "c5": 70.4e6 + 2.2e6,     # w8a16_splitk_kernel<SILU>
 }
 
 

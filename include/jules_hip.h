@@ -137,9 +137,11 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale,
  * Constraints: 1 <= M <= 16, N % 16 == 0, K % 8 == 0; W and x 16-byte
  * aligned, y 8-byte aligned.
  * workspace: device memory of at least jules_hip_w8a16_workspace_size(M,N,K)
- * bytes, 16-byte aligned (fp32 split-K partials, KS x M x N with KS <= 16);
- * it needs no initialisation and is overwritten by every call.  Calls that
- * overlap in time need separate workspaces.
+ * bytes, 16-byte aligned (fp32 split-K partial tiles, KS x ceil(N/256) x
+ * 16 KiB with KS <= 8, then one 8-byte flag per tile and split; one launch
+ * does the split-K reduction); it needs no initialisation and is
+ * overwritten by every call.  Calls that overlap in time need separate
+ * workspaces.
  * No reference counterpart: the reference's int8 kernel (matmulInt8,
  * FusedKernels.h:867) is W8A8 with one scalar scale; routed name
  * "matmulW8A16BiasSilu" is new.

@@ -21,13 +21,15 @@
 // Work split: a workgroup (8 waves) owns 256 columns and one of KS K-ranges;
 // every wave takes its own 32-row k-steps of that range, issuing all of its
 // weight loads for 2 k-steps before converting the first.  The 8 wave
-// partials are summed in LDS in a fixed tree order and the workgroup stores
-// its fp32 partial tile to the workspace.  A second, small kernel sums the KS
-// partials of every output in split order and applies scale, bias and the
-// activation.  The kernel boundary makes the partials visible; an agent-scope
-// release fence per workgroup (an L2 write-back on this part) measured
-// several microseconds.  The summation order is fixed, so results are
-// deterministic run to run.
+// partials are summed in LDS in wave order and the workgroup stores its fp32
+// partial tile to the workspace.  The last of the KS workgroups of a
+// column tile to finish (found through per-call flags in the workspace) sums
+// the KS partials of the tile in split order and applies scale, bias and the
+// activation, so one launch does the whole operation.  The summation order is
+// fixed, so results are deterministic run to run.
+#include <atomic>
+#include <random>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -39,6 +41,9 @@ constexpr int WAVES = 8;
 constexpr int THREADS = WAVES * 64;
 constexpr int KSTEP = 32;       // rows per MFMA k-step
 constexpr int GROUP = 2;        // k-steps whose loads are in flight together
+constexpr int MAX_KS = 8;       // most K splits (partials) per output
+// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt unconstrained (gfx9 encoding)
+constexpr unsigned kWaitVm0 = 0x0F70;
 
 struct Plan {
     int ks;         // number of K splits (partials)
@@ -49,19 +54,42 @@ inline Plan plan(int K) {
     const int total_steps = (K + KSTEP - 1) / KSTEP;
     // aim for two groups of GROUP k-steps per wave (measured best at
     // K = N = 8192: fewer splits starve the chip, more cost partial traffic);
-    // at most 16 splits
+    // at most MAX_KS splits (larger K gives each wave more k-steps)
     int ks = (total_steps + 2 * WAVES * GROUP - 1) / (2 * WAVES * GROUP);
-    if (ks > 16) ks = 16;
+    if (ks > MAX_KS) ks = MAX_KS;
     if (ks < 1) ks = 1;
     const int per_split = (total_steps + ks - 1) / ks;
     const int steps = (per_split + WAVES - 1) / WAVES;
     return {ks, steps};
 }
 
-__global__ __launch_bounds__(THREADS, 1) void w8a16_partial_kernel(
+// cache policy bits of buffer instructions: sc1 (coherent at agent scope)
+constexpr int kSc1 = 16;
+constexpr int PART_FLOATS = 16 * 64 * 4;  // one (split, tile) partial: [j][lane] x 4 rows
+
+// Workgroup barrier that orders LDS accesses only: global loads and stores
+// stay in flight across it (__syncthreads() waits for them to complete).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// buffer resource over the partial tile of (split, tile); an empty range
+// (loads return 0, stores are dropped) when !valid
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* partials, int split, int tiles,
+                                                           int tile, bool valid) {
+    return __builtin_amdgcn_make_buffer_rsrc(partials + ((int64_t)split * tiles + tile) * PART_FLOATS,
+                                             0, valid ? PART_FLOATS * 4 : 0, 0x00020000);
+}
+
+template <int ACT>
+__global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ W, int M, int N, int K, int KS,
-    int steps, float* __restrict__ partials) {
-    __shared__ f32x4_t red[4 * 16 * 64];  // 4 wave slots x 16 accumulators x 64 lanes
+    int steps, float* __restrict__ partials, const float* __restrict__ scale,
+    const float* __restrict__ bias, uint16_t* __restrict__ y, uint64_t* __restrict__ flags,
+    uint64_t call_id) {
+    __shared__ f32x4_t red[WAVES * 16 * 64];  // 128 KiB: [wave][j][lane]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = blockIdx.x, split = blockIdx.y;
@@ -73,6 +101,17 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_partial_kernel(
     f32x4_t acc[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // scale and bias of the two columns this lane finishes if its workgroup
+    // reduces the tile (see the reducer below), loaded now so that their
+    // latency is off the tail
+    float sc[2], bi[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = min(n0 + 16 * lc + 2 * wave + h, N - 1);
+        sc[h] = scale[c];
+        bi[h] = bias ? bias[c] : 0.0f;
+    }
 
     // k-steps of this split: [s0, s1); wave w takes s0 + w + WAVES * t
     const int total_steps = (K + KSTEP - 1) / KSTEP;
@@ -128,79 +167,144 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_partial_kernel(
         }
     }
 
-    // ---- fixed-order tree reduction of the 8 wave partials in LDS ----
-    // slot layout red[slot][j][lane]: a wave's 64 lanes write 1 KiB contiguously
-    auto put = [&](int slot) {
+    // ---- reduction of the 8 wave partials in LDS ----
+    // Every wave writes its 16 accumulators ([wave][j][lane]: 1 KiB
+    // contiguous per instruction); then wave w sums accumulators j = 2w and
+    // 2w+1 over the 8 waves in wave order and owns that part of the
+    // workgroup's partial tile from here on.
 #pragma unroll
-        for (int j = 0; j < 16; ++j) red[(slot * 16 + j) * 64 + lane] = acc[j];
-    };
-    auto add = [&](int slot) {
+    for (int j = 0; j < 16; ++j) red[(wave * 16 + j) * 64 + lane] = acc[j];
+    lds_barrier();
+    f32x4_t r[2];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[j] += red[(slot * 16 + j) * 64 + lane];
-    };
-    if (wave >= 4) put(wave - 4);
-    __syncthreads();
-    if (wave < 4) add(wave);
-    __syncthreads();
-    if (wave >= 2 && wave < 4) put(wave - 2);
-    __syncthreads();
-    if (wave < 2) add(wave);
-    __syncthreads();
-    if (wave == 1) put(0);
-    __syncthreads();
-    if (wave != 0) return;
-    add(0);
-    // 16x16 output layout: lane holds rows 4*lg + i, column n' = lc of
-    // MFMA j, i.e. global column col0 + j
-    float* part = partials + (int64_t)split * M * N;
+    for (int h = 0; h < 2; ++h) {
+        const int j = 2 * wave + h;
+        r[h] = red[j * 64 + lane];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * lg + i;
-        if (m < M && col_ok) {
+        for (int w = 1; w < WAVES; ++w) r[h] += red[(w * 16 + j) * 64 + lane];
+    }
+
+    // ---- partial tile out, then the last workgroup of the column tile ----
+    // Partials and flags are shared between workgroups on different XCDs,
+    // whose L2s are not coherent with each other.  Every access to them
+    // carries sc1 (coherent at agent scope: the cache policy of the
+    // compiler's agent-scope atomics), so no L2 write-back or invalidate is
+    // needed, and the order between them comes from waiting for the waves'
+    // own memory operations to complete (vmcnt(0)): the waits of the
+    // compiler's agent-scope seq_cst sequences, minus their L2 write-back and
+    // invalidate, which exist only for plain (non-coherent) data.  An
+    // earlier version released the partials with __threadfence(); its L2
+    // write-back (buffer_wbl2) cost more than a separate reduction kernel.
+    //
+    // A partial tile is stored in the MFMA accumulator layout, [j][lane] x 16
+    // bytes (16 KiB per (split, tile)), so each store instruction writes
+    // whole cache lines: write-through stores of scattered 8-byte pieces cost
+    // a line transfer each.
+    //
+    // Protocol per workgroup: every wave waits for its partial stores to
+    // complete; then wave 0 stores flags[tile][split] = call_id, waits, and
+    // loads the tile's KS flags.  The workgroup whose flag store completes
+    // last sees every flag equal to call_id (each load is issued after its
+    // own flag store completed), so some workgroup reduces; if several do,
+    // they write the same bits (same partials, summed in split order).
+    // call_id is new for every call, so flags from earlier calls or
+    // uninitialised workspace never match.
+    const int tiles = gridDim.x;
+    const int lanes_live = 16 * ((M + 3) / 4);  // lanes holding rows < M
+    const bool live = lane < lanes_live;
+    {
+        const __amdgpu_buffer_rsrc_t pr = part_rsrc(partials, split, tiles, tile, true);
+        if (live) {
 #pragma unroll
-            for (int j4 = 0; j4 < 4; ++j4) {
-                f32x4_t v = {acc[4 * j4][i], acc[4 * j4 + 1][i], acc[4 * j4 + 2][i], acc[4 * j4 + 3][i]};
-                *reinterpret_cast<f32x4_t*>(part + (int64_t)m * N + col0 + 4 * j4) = v;
+            for (int h = 0; h < 2; ++h)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, r[h]), pr,
+                                                       ((2 * wave + h) * 64 + lane) * 16, 0, kSc1);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's partial stores are done
+    __shared__ int last;
+    lds_barrier();                        // ... and every wave's
+    if (wave == 0) {
+        uint64_t* tf = flags + (int64_t)tile * KS;
+        if (lane == 0) __hip_atomic_store(tf + split, call_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        const uint64_t f =
+            lane < KS ? __hip_atomic_load(tf + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : call_id;
+        const bool all = __builtin_amdgcn_ballot_w64(f != call_id) == 0;
+        if (lane == 0) last = all;
+    }
+    lds_barrier();
+    if (!last || !live) return;
+
+    // ---- reducer: y = act(scale * sum_p partials[p] + bias) for the tile ----
+    // Wave w finishes accumulators j = 2w, 2w+1: lane (lc, lg) holds rows
+    // 4*lg.. of column n0 + 16*lc + j.  The other splits' partials are
+    // loaded (contiguous across lanes), its own is r[]; the sum is taken in
+    // split order.  The loads are branch-free: a split that is absent or
+    // this workgroup's own gets an empty buffer range (the load returns 0
+    // without touching memory) and is replaced by a select, so the code
+    // stays short.
+    f32x4_t pv[2][MAX_KS];
+#pragma unroll
+    for (int p = 0; p < MAX_KS; ++p) {
+        const __amdgpu_buffer_rsrc_t pr = part_rsrc(partials, p, tiles, tile, p < KS && p != split);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            pv[h][p] = __builtin_bit_cast(
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(pr, ((2 * wave + h) * 64 + lane) * 16, 0, kSc1));
+    }
+    // keep every load here, in flight together (the compiler would otherwise
+    // sink some into the conditional sums below and wait for each in turn)
+#pragma unroll
+    for (int p = 0; p < MAX_KS; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(pv[h][p]));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = n0 + 16 * lc + 2 * wave + h;
+        f32x4_t sum = split == 0 ? r[h] : pv[h][0];
+#pragma unroll
+        for (int p = 1; p < MAX_KS; ++p) {
+            const f32x4_t v = p == split ? r[h] : pv[h][p];
+            if (p < KS) sum += v;
+        }
+        if (c >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * lg + i;
+            if (m < M) {
+                float t = sum[i] * sc[h];
+                if (bias) t = t + bi[h];
+                y[(int64_t)m * N + c] = __builtin_bit_cast(uint16_t, (__bf16)activate<ACT>(t));
             }
         }
     }
 }
 
-// y = act(scale * sum_p partials[p] + bias): each thread 4 consecutive
-// columns of one row, all KS partial loads issued before the first add, the
-// sum taken in split order.
-template <int ACT>
-__global__ __launch_bounds__(256) void w8a16_finalize_kernel(
-    const float* __restrict__ partials, const float* __restrict__ scale,
-    const float* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int KS) {
-    const int64_t e0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
-    if (e0 >= (int64_t)M * N) return;
-    const int m = (int)(e0 / N), c = (int)(e0 % N);
-    f32x4_t part[16];
-#pragma unroll
-    for (int p = 0; p < 16; ++p)
-        if (p < KS) part[p] = *reinterpret_cast<const f32x4_t*>(partials + ((int64_t)p * M + m) * N + c);
-    f32x4_t sum = part[0];
-#pragma unroll
-    for (int p = 1; p < 16; ++p)
-        if (p < KS) sum += part[p];
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float t = sum[i] * scale[c + i];
-        if (bias) t = t + bias[c + i];
-        v[i] = activate<ACT>(t);
-    }
-    u32x2_t o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    *reinterpret_cast<u32x2_t*>(y + (int64_t)m * N + c) = o;
-}
-
 }  // namespace
 
+// workspace: KS x tiles partial tiles of PART_FLOATS fp32 each, then one
+// 64-bit flag per (column tile, split)
 size_t w8a16_workspace_size(int M, int N, int K) {
+    (void)M;
     const Plan p = plan(K);
-    return (size_t)p.ks * M * N * sizeof(float);
+    const size_t tiles = (size_t)(N + COLS - 1) / COLS;
+    return tiles * p.ks * (PART_FLOATS * sizeof(float) + sizeof(uint64_t));
 }
+
+namespace {
+// A value no earlier call of this process used: a per-process random start
+// plus a call counter (flags left in a workspace by other processes or by
+// earlier calls differ from it).
+uint64_t next_call_id() {
+    static const uint64_t start = [] {
+        std::random_device rd;
+        return ((uint64_t)rd() << 32) ^ (uint64_t)rd() ^ (uint64_t)(uintptr_t)&rd;
+    }();
+    static std::atomic<uint64_t> counter{0};
+    return start + counter.fetch_add(1, std::memory_order_relaxed) + 1;
+}
+}  // namespace
 
 hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float* scale,
                         const float* bias, uint16_t* y, int M, int N, int K, void* ws,
@@ -208,15 +312,12 @@ hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float
     const Plan p = plan(K);
     const int tiles = (N + COLS - 1) / COLS;
     float* partials = static_cast<float*>(ws);
-    hipLaunchKernelGGL(w8a16_partial_kernel, dim3(tiles, p.ks), dim3(THREADS), 0, s, x, W, M, N,
-                       K, p.ks, p.steps, partials);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int64_t quads = ((int64_t)M * N) / 4;  // N % 16 == 0
-    const unsigned blocks = (unsigned)((quads + 255) / 256);
+    uint64_t* flags = reinterpret_cast<uint64_t*>(partials + (size_t)tiles * p.ks * PART_FLOATS);
+    const uint64_t id = next_call_id();
+    hipError_t e = hipSuccess;
     JH_DISPATCH_ACT(act, ACT, {
-        hipLaunchKernelGGL(w8a16_finalize_kernel<ACT>, dim3(blocks), dim3(256), 0, s, partials,
-                           scale, bias, y, M, N, p.ks);
+        hipLaunchKernelGGL(w8a16_splitk_kernel<ACT>, dim3(tiles, p.ks), dim3(THREADS), 0, s, x, W, M,
+                           N, K, p.ks, p.steps, partials, scale, bias, y, flags, id);
         e = hipGetLastError();
     });
     return e;

@@ -95,6 +95,66 @@ def test_deterministic_and_workspace_reuse(dev):
     assert torch.equal(a, _w8(dev, x, W, scale, bias, "silu", ws))
 
 
+def test_split_reduction_bit_exact_from_partials(dev):
+    """The split-K reduction, checked bit for bit: after a call the workspace
+    still holds the KS fp32 partial tiles, and y must equal
+    bf16(act(((p0 + p1) + ... + p_{KS-1}) * scale + bias)) computed from them
+    in fp32 on the host, in split order."""
+    case("w8a16 split reduction from workspace partials")
+    M, N, K = 8, 8192, 8192
+    x, W, scale, bias = I.w8a16_inputs(M, N, K, seed=11)
+    ws = ops.w8a16_workspace(M, N, K, dev)
+    # workspace = [KS][tiles] partial tiles of 16 KiB, each in the MFMA
+    # accumulator layout [j 16][lane 64][row-in-group 4] fp32 (lane = 16*lg +
+    # lc holds rows 4*lg.., column 16*lc + j of the 256-column tile), then one
+    # 8-byte flag per (tile, split)
+    tiles = N // 256
+    KS = ws.numel() // (tiles * (16384 + 8))
+    assert ws.numel() == KS * tiles * (16384 + 8) and 1 <= KS <= 16
+
+    def partials():
+        a = ws[:KS * tiles * 16384].view(torch.float32).cpu().numpy()
+        a = a.reshape(KS, tiles, 16, 4, 16, 4).transpose(0, 3, 5, 1, 4, 2)
+        return a.reshape(KS, 16, tiles * 256)[:, :M, :N]
+
+    for act, b in (("silu", bias), ("gelu", None)):
+        y = _w8(dev, x, W, scale, b, act, ws).view(torch.int16).cpu().numpy().view(np.uint16)
+        parts = partials()
+        s = parts[0].copy()
+        for p in range(1, KS):
+            s = s + parts[p]
+        pre = s * scale
+        if b is not None:
+            pre = pre + b
+        np.testing.assert_array_equal(y, I.bf16_bits(po.act_array(act, pre)), err_msg=act)
+        # and the partials are those of the product
+        assert I.rel_err(parts.sum(0, dtype=np.float64), po.w8a16_64(x, W, np.ones_like(scale),
+                                                                     None, "none")) < 1e-5
+
+
+def test_alternating_calls_same_workspace(dev):
+    """Back-to-back calls with different inputs on one workspace: every result
+    equals that input's first result, so no call reads another call's
+    partials or flags.  Every fifth call first overwrites the workspace."""
+    case("w8a16 alternating calls, one workspace")
+    M, N, K = 8, 8192, 8192
+    ws = ops.w8a16_workspace(M, N, K, dev)
+    ins = [I.w8a16_inputs(M, N, K, seed=s) for s in (21, 22)]
+    dev_ins = [(to_dev(x, torch.bfloat16, dev), to_dev(W, torch.int8, dev),
+                to_dev(sc, torch.float32, dev), to_dev(b, torch.float32, dev))
+               for x, W, sc, b in ins]
+    first = [ops.w8a16_gemm(*t, "silu", workspace=ws) for t in dev_ins]
+    for (x, W, sc, b), y in zip(ins, first):
+        assert I.rel_err(to_np(y), po.w8a16_64(x, W, sc, b, "silu")) < I.TOL["bf16"]
+    outs = []
+    for i in range(60):
+        if i % 5 == 4:
+            ws.fill_(i)
+        outs.append(ops.w8a16_gemm(*dev_ins[i % 2], "silu", workspace=ws))
+    for i, y in enumerate(outs):
+        assert torch.equal(y, first[i % 2]), f"call {i}"
+
+
 def test_registry_path(dev):
     case("w8a16 registry matmulW8A16BiasSilu")
     x, W, scale, bias = I.w8a16_inputs(4, 512, 512, seed=9)
