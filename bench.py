@@ -9,7 +9,8 @@ synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 
 The same run also times every BASELINE config on its own (per_config, keys
 c1-c5), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
-entropy, GB/s against HBM), the dominant kernel against its roofline
+entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
+(per_config, keys m1-m2, fp32 TFLOP/s), the dominant kernel against its roofline
 (roofline), and the CPU port of the reference AVX-512 path on a bounded
 sample (cpu_baseline).
 
@@ -73,6 +74,22 @@ ROW_CONFIGS = {
 }
 
 
+# The 2-layer MLP forward + loss + backward (interleavedMLPForwardBackward):
+# the reference benchmark's shape (bench_kernel.cpp:268-271, launch-latency
+# bound on a GPU) and a large one where the fp32 MFMA GEMMs dominate.
+MLP_CONFIGS = {
+    "m1": dict(kind="mlp", M=64, K1=784, N1=256, N2=10),
+    "m2": dict(kind="mlp", M=8192, K1=4096, N1=4096, N2=1024),
+}
+
+
+def mlp_flops(spec):
+    """Forward 2M(K1 N1 + N1 N2); backward dW2, dA, dW1, dX: 2M(N1 N2 + N1 N2
+    + K1 N1 + K1 N1)."""
+    M, K1, N1, N2 = spec["M"], spec["K1"], spec["N1"], spec["N2"]
+    return 6.0 * M * N1 * (K1 + N2)
+
+
 def row_bytes(spec):
     """Algorithmic HBM bytes: the fp32 rows read once and written once, plus
     gamma/beta (layernorm) or targets and the loss (cross entropy)."""
@@ -132,6 +149,15 @@ class Runner:
                 self.ws = ops.cross_entropy_workspace(M, dev)
             self.work = row_bytes(s)
             self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK["hbm"]
+        elif s["kind"] == "mlp":
+            M, K1, N1, N2 = s["M"], s["K1"], s["N1"], s["N2"]
+            u = lambda *shape: torch.rand(shape, generator=g, device=dev) * 2 - 1
+            self.X, self.W1, self.b1 = u(M, K1), u(K1, N1) / K1 ** 0.5, u(N1)
+            self.W2, self.b2 = u(N1, N2) / N1 ** 0.5, u(N2)
+            self.t = torch.randint(0, N2, (M,), generator=g, device=dev, dtype=torch.int32)
+            self.ws = ops.mlp_workspace(M, K1, N1, N2, dev)
+            self.work = mlp_flops(s)
+            self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK["f32"]
         else:
             M, N, K = s["M"], s["N"], s["K"]
             # 64 MiB of weights fits in the 256 MB MALL: rotate 8 distinct
@@ -160,6 +186,9 @@ class Runner:
             ops.layernorm(self.x, self.gamma, self.beta, out=self.y)
         elif s["kind"] == "xent":
             ops.cross_entropy(self.x, self.t, grad=self.y, loss=self.loss, workspace=self.ws)
+        elif s["kind"] == "mlp":
+            ops.mlp_forward_backward(self.X, self.W1, self.b1, self.W2, self.b2, self.t,
+                                     with_dX=True, workspace=self.ws)
         else:
             ops.w8a16_gemm(self.x, self.W[self.i % self.nw], self.scale, self.bias, s["act"],
                            out=self.y, workspace=self.ws)
@@ -341,7 +370,7 @@ def main():
 
     # ---- per-config launch timings -----------------------------------------
     per = {}
-    ALL = {**CONFIGS, **ROW_CONFIGS}
+    ALL = {**CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS}
     names = [n for n in ALL if not args.only or n in args.only.split(",")]
     if args.step_only:
         names = []
@@ -349,7 +378,7 @@ def main():
         log(f"config {name} {ALL[name]}")
         try:
             r = Runner(name, ALL[name], dev)
-            iters = 20 if name in ("c3", "c4") else 50
+            iters = 20 if name in ("c3", "c4", "m2") else 50
             durs, _ = time_launches([r], 5, iters)
             d = sorted(durs[0])
             med = statistics.median(d)

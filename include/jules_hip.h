@@ -220,6 +220,32 @@ int jules_hip_cross_entropy(const float* logits, const int32_t* targets,
                             void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* ---- 2-layer MLP forward + loss + backward --------------------------------
+ * Replaces interleavedMLPForwardBackward (include/jules/Kernel/
+ * InterleavedAutodiff.h:55-62): same operands in the same order, minus the
+ * ExecutionArena/TilePlanner, plus loss/workspace/stream.  fp32 row-major:
+ * X [M,K1], W1 [K1,N1], b1 [N1], W2 [N1,N2], b2 [N2], targets [M] int32.
+ *   output [M,N2] = relu(X W1 + b1) W2 + b2
+ *   *loss (device float) = mean_i -log(softmax(output_i)[t_i] + 1e-10)
+ *   dW1 [K1,N1], db1 [N1], dW2 [N1,N2], db2 [N2]: gradients of the loss
+ *   dX [M,K1] or NULL
+ * Gradients are overwritten (the reference zeroes them first).  A target
+ * outside [0,N2) gives a NaN row loss and no one-hot term, as in
+ * jules_hip_cross_entropy.  M = 0 zeroes the gradients and writes a NaN loss
+ * (the reference's 0/0).  Deterministic.
+ * workspace: jules_hip_mlp_workspace_size(M,K1,N1,N2) bytes, 16-byte aligned
+ * (activations, dO, dH, row losses, column-sum partials); no initialisation.
+ * Routed name "interleavedMLPForwardBackward" (KernelRoutingPass.h:21):
+ * (X, W1, b1, W2, b2, targets) -> (output, dW1, db1, dW2, db2, loss[, dX]).
+ */
+size_t jules_hip_mlp_workspace_size(int M, int K1, int N1, int N2);
+int jules_hip_mlp_forward_backward(const float* X, const float* W1, const float* b1,
+                                   const float* W2, const float* b2, const int32_t* targets,
+                                   float* output, float* dW1, float* db1, float* dW2,
+                                   float* db2, float* dX, int M, int K1, int N1, int N2,
+                                   float* loss, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 /* ---- MFMA calibration -----------------------------------------------------
  * No counterpart in the reference: a roofline calibration for callers that
  * report MFMA rates against the rate the part sustains under load (its engine

@@ -111,6 +111,27 @@ void fusedLayerNorm(float* output, const float* input, const float* gamma, const
                     int M, int N, float epsilon = 1e-5f);
 // reference FusedKernels.h:766; returns the mean loss (NaN on failure)
 float fusedCrossEntropyLoss(const float* logits, const int32_t* targets, float* grad, int M, int N);
+// reference InterleavedAutodiff.h:41-53
+struct MLPGradients {
+    float* dW1;
+    float* db1;
+    float* dW2;
+    float* db2;
+    float* dX;
+};
+struct InterleavedMLPResult {
+    float loss;
+    MLPGradients grads;
+};
+// reference InterleavedAutodiff.h:55-62: 2-layer MLP forward, softmax cross
+// entropy and backward; dX may be null; loss is NaN on failure
+InterleavedMLPResult interleavedMLPForwardBackward(const float* X, const float* W1,
+                                                   const float* b1, const float* W2,
+                                                   const float* b2, const int32_t* targets,
+                                                   float* output, float* dW1, float* db1,
+                                                   float* dW2, float* db2, float* dX, int M,
+                                                   int K1, int N1, int N2, ExecutionArena& arena,
+                                                   TilePlanner& planner);
 // reference FusedKernels.h:867 (scalar-path semantics)
 void matmulInt8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K, float scale_A,
                 float scale_B, const float* bias = nullptr, ExecutionArena* arena = nullptr);

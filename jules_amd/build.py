@@ -26,7 +26,7 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
           "-munsafe-fp-atomics"]
 
 SOURCES = ["gemm_f32.hip", "gemm_bf16.hip", "flash_fwd.hip", "w8a16.hip", "matmul_int8.hip",
-           "rowops.hip", "calib.hip", "pjrt_ops.hip", "capi.cpp", "kernel_shims.cpp",
+           "rowops.hip", "mlp.hip", "calib.hip", "pjrt_ops.hip", "capi.cpp", "kernel_shims.cpp",
            "pjrt.cpp"]
 
 
@@ -63,18 +63,23 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
 
 
 def _build_selftests(verbose):
-    """Host-only C++ test programs linked against the library (g++)."""
-    src = os.path.join(ROOT, "tests", "cpp", "pjrt_selftest.cpp")
-    if not os.path.exists(src):
+    """Host-only C++ test programs tests/cpp/<name>_selftest.cpp, linked
+    against the library (g++)."""
+    cdir = os.path.join(ROOT, "tests", "cpp")
+    if not os.path.isdir(cdir):
         return
-    out = os.path.join(ROOT, "tests", "cpp", "pjrt_selftest")
-    cmd = ["g++", "-O2", "-std=c++17", f"-I{INCLUDE}", src, f"-L{HERE}", "-ljules_hip",
-           "-Wl,-rpath,$ORIGIN/../../jules_amd", "-o", out]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"g++ failed on {src}:\n{r.stdout}\n{r.stderr}")
+    for f in sorted(os.listdir(cdir)):
+        if not f.endswith("_selftest.cpp"):
+            continue
+        src = os.path.join(cdir, f)
+        out = os.path.join(cdir, f[:-4])
+        cmd = ["g++", "-O2", "-std=c++17", f"-I{INCLUDE}", src, f"-L{HERE}", "-ljules_hip",
+               "-Wl,-rpath,$ORIGIN/../../jules_amd", "-o", out]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"g++ failed on {src}:\n{r.stdout}\n{r.stderr}")
 
 
 if __name__ == "__main__":

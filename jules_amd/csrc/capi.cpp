@@ -264,6 +264,38 @@ int jules_hip_cross_entropy(const float* logits, const int32_t* targets, float* 
                      "cross_entropy launch");
 }
 
+size_t jules_hip_mlp_workspace_size(int M, int K1, int N1, int N2) {
+    if (M < 0 || K1 < 1 || N1 < 1 || N2 < 1) return 0;
+    return jh::mlp_workspace_size(M, K1, N1, N2);
+}
+
+int jules_hip_mlp_forward_backward(const float* X, const float* W1, const float* b1,
+                                   const float* W2, const float* b2, const int32_t* targets,
+                                   float* output, float* dW1, float* db1, float* dW2, float* db2,
+                                   float* dX, int M, int K1, int N1, int N2, float* loss,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    if (M < 0 || K1 < 1 || N1 < 1 || N2 < 1)
+        return fail(JH_ERR_SHAPE, "mlp: needs M >= 0 and K1, N1, N2 >= 1 (got %d %d %d %d)", M, K1,
+                    N1, N2);
+    if ((int64_t)M * K1 > kMaxElems || (int64_t)M * N1 > kMaxElems || (int64_t)M * N2 > kMaxElems ||
+        (int64_t)K1 * N1 > kMaxElems || (int64_t)N1 * N2 > kMaxElems)
+        return fail(JH_ERR_SHAPE, "mlp: too large");
+    if (!W1 || !b1 || !W2 || !b2 || !dW1 || !db1 || !dW2 || !db2 || !loss)
+        return fail(JH_ERR_NULL, "mlp: null weight, bias, gradient or loss pointer");
+    if (M > 0 && (!X || !targets || !output)) return fail(JH_ERR_NULL, "mlp: null X, targets or output");
+    const void* ptrs[] = {X, W1, b1, W2, b2, targets, output, dW1, db1, dW2, db2, dX, loss};
+    for (const void* q : ptrs)
+        if (!aligned(q, 4)) return fail(JH_ERR_ALIGN, "mlp: operands must be 4-byte aligned");
+    const size_t need = jh::mlp_workspace_size(M, K1, N1, N2);
+    if (M > 0 && (!workspace || workspace_bytes < need))
+        return fail(JH_ERR_WORKSPACE, "mlp: workspace %zu bytes, need %zu", workspace_bytes, need);
+    if (!aligned(workspace, 16)) return fail(JH_ERR_ALIGN, "mlp: workspace alignment");
+    return check_hip(jh::launch_mlp_forward_backward(X, W1, b1, W2, b2, targets, output, dW1, db1,
+                                                     dW2, db2, dX, loss, M, K1, N1, N2, workspace,
+                                                     static_cast<hipStream_t>(stream)),
+                     "mlp launch");
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
@@ -566,6 +598,44 @@ int k_cross_entropy(int ni, const jh_tensor* in, int no, jh_tensor* out, const c
                                    static_cast<float*>(addr_mut(l)), (int)M, (int)N, ws, need, s);
 }
 
+int k_mlp(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
+    if (ni != 6 || (no != 6 && no != 7) || !in || !out)
+        return fail(JH_ERR_ARG, "interleavedMLPForwardBackward: (X, W1, b1, W2, b2, targets) -> "
+                                "(output, dW1, db1, dW2, db2, loss[, dX])");
+    const jh_tensor &x = in[0], &w1 = in[1], &b1 = in[2], &w2 = in[3], &b2 = in[4], &t = in[5];
+    for (int i = 0; i < ni; ++i)
+        if (!contiguous(in[i])) return fail(JH_ERR_SHAPE, "interleavedMLPForwardBackward: contiguous inputs");
+    for (int i = 0; i < no; ++i)
+        if (!contiguous(out[i]) || out[i].dtype != JH_F32)
+            return fail(JH_ERR_SHAPE, "interleavedMLPForwardBackward: contiguous fp32 outputs");
+    if (x.rank != 2 || w1.rank != 2 || w2.rank != 2)
+        return fail(JH_ERR_SHAPE, "interleavedMLPForwardBackward: X, W1, W2 rank 2");
+    for (int i = 0; i < 5; ++i)
+        if (in[i].dtype != JH_F32) return fail(JH_ERR_DTYPE, "interleavedMLPForwardBackward: fp32 X, W, b");
+    if (t.dtype != JH_I32) return fail(JH_ERR_DTYPE, "interleavedMLPForwardBackward: int32 targets");
+    const int64_t M = x.sizes[0], K1 = x.sizes[1], N1 = w1.sizes[1], N2 = w2.sizes[1];
+    if (w1.sizes[0] != K1 || w2.sizes[0] != N1 || numel(b1) != N1 || numel(b2) != N2 ||
+        numel(t) != M || numel(out[0]) != M * N2 || numel(out[1]) != K1 * N1 ||
+        numel(out[2]) != N1 || numel(out[3]) != N1 * N2 || numel(out[4]) != N2 ||
+        numel(out[5]) != 1 || (no == 7 && numel(out[6]) != M * K1))
+        return fail(JH_ERR_SHAPE, "interleavedMLPForwardBackward: operand shapes disagree");
+    if (M > INT32_MAX || K1 > INT32_MAX || N1 > INT32_MAX || N2 > INT32_MAX)
+        return fail(JH_ERR_SHAPE, "interleavedMLPForwardBackward: too large");
+    const size_t need = jules_hip_mlp_workspace_size((int)M, (int)K1, (int)N1, (int)N2);
+    void* ws = nullptr;
+    if (need > 0) {
+        const int st = registry_workspace(need, &ws);
+        if (st != JH_OK) return st;
+    }
+    float* f[7];
+    for (int i = 0; i < no; ++i) f[i] = static_cast<float*>(addr_mut(out[i]));
+    return jules_hip_mlp_forward_backward(
+        static_cast<const float*>(addr(x)), static_cast<const float*>(addr(w1)),
+        static_cast<const float*>(addr(b1)), static_cast<const float*>(addr(w2)),
+        static_cast<const float*>(addr(b2)), static_cast<const int32_t*>(addr(t)), f[0], f[1], f[2],
+        f[3], f[4], no == 7 ? f[6] : nullptr, (int)M, (int)K1, (int)N1, (int)N2, f[5], ws, need, s);
+}
+
 struct Entry {
     const char* name;
     jh_kernel_fn fn;
@@ -588,6 +658,7 @@ const Entry kRegistry[] = {
     {"fusedSoftmax", k_softmax},
     {"fusedLayerNorm", k_layernorm},
     {"fusedCrossEntropyLoss", k_cross_entropy},
+    {"interleavedMLPForwardBackward", k_mlp},
     {"fusedMatmul", k_matmul},
     {"fusedMatmulBias", k_matmul_bias},
     {"fusedMatmulBiasGelu", k_matmul_bias_gelu},

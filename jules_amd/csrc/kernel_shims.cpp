@@ -224,6 +224,53 @@ void fusedLayerNorm(float* output, const float* input, const float* gamma, const
     record(st);
 }
 
+InterleavedMLPResult interleavedMLPForwardBackward(const float* X, const float* W1,
+                                                   const float* b1, const float* W2,
+                                                   const float* b2, const int32_t* targets,
+                                                   float* output, float* dW1, float* db1,
+                                                   float* dW2, float* db2, float* dX, int M,
+                                                   int K1, int N1, int N2, ExecutionArena&,
+                                                   TilePlanner&) {
+    const float nan = std::numeric_limits<float>::quiet_NaN();
+    InterleavedMLPResult res{nan, MLPGradients{dW1, db1, dW2, db2, dX}};
+    if (M < 0 || K1 < 1 || N1 < 1 || N2 < 1) {
+        record(JH_ERR_SHAPE);
+        return res;
+    }
+    const size_t f = sizeof(float), m = (size_t)M, k1 = (size_t)K1, n1 = (size_t)N1,
+                 n2 = (size_t)N2;
+    float loss = nan;
+    std::vector<char> ws_host(std::max<size_t>(16, jules_hip_mlp_workspace_size(M, K1, N1, N2)));
+    DevBuf x(X, f * m * k1, true, false), w1(W1, f * k1 * n1, true, false),
+        bb1(b1, f * n1, true, false), w2(W2, f * n1 * n2, true, false), bb2(b2, f * n2, true, false),
+        t(targets, sizeof(int32_t) * m, true, false), o(output, f * m * n2, false, true),
+        g1(dW1, f * k1 * n1, false, true), gb1(db1, f * n1, false, true),
+        g2(dW2, f * n1 * n2, false, true), gb2(db2, f * n2, false, true),
+        gx(dX, f * m * k1, false, true), l(&loss, f, false, true),
+        ws(ws_host.data(), ws_host.size(), false, false);
+    const DevBuf* all[] = {&x, &w1, &bb1, &w2, &bb2, &t, &o, &g1, &gb1, &g2, &gb2, &gx, &l, &ws};
+    for (const DevBuf* d : all)
+        if (!d->ok()) {
+            record(JH_ERR_HIP);
+            return res;
+        }
+    int st = jules_hip_mlp_forward_backward(
+        static_cast<const float*>(x.get()), static_cast<const float*>(w1.get()),
+        static_cast<const float*>(bb1.get()), static_cast<const float*>(w2.get()),
+        static_cast<const float*>(bb2.get()), static_cast<const int32_t*>(t.get()),
+        static_cast<float*>(o.get()), static_cast<float*>(g1.get()), static_cast<float*>(gb1.get()),
+        static_cast<float*>(g2.get()), static_cast<float*>(gb2.get()),
+        dX ? static_cast<float*>(gx.get()) : nullptr, M, K1, N1, N2, static_cast<float*>(l.get()),
+        ws.get(), ws_host.size(), nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    DevBuf* outs[] = {&o, &g1, &gb1, &g2, &gb2, &gx, &l};
+    for (DevBuf* d : outs)
+        if (st == JH_OK && !d->finish()) st = JH_ERR_HIP;
+    record(st);
+    if (st == JH_OK) res.loss = loss;
+    return res;
+}
+
 float fusedCrossEntropyLoss(const float* logits, const int32_t* targets, float* grad, int M,
                             int N) {
     const float nan = std::numeric_limits<float>::quiet_NaN();

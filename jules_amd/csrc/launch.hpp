@@ -32,6 +32,14 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
 hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, float* grad,
                                 float* loss, float* row_loss, int M, int N, hipStream_t s);
 
+// 2-layer MLP forward + softmax cross entropy + backward (mlp.hip)
+size_t mlp_workspace_size(int M, int K1, int N1, int N2);
+hipError_t launch_mlp_forward_backward(const float* X, const float* W1, const float* b1,
+                                       const float* W2, const float* b2, const int32_t* targets,
+                                       float* output, float* dW1, float* db1, float* dW2, float* db2,
+                                       float* dX, float* loss, int M, int K1, int N1, int N2,
+                                       void* ws, hipStream_t s);
+
 // PJRT executor ops (pjrt_ops.hip): fp32, rank <= 8
 enum PjOp {
     PJ_ADD = 0, PJ_SUB, PJ_MUL, PJ_DIV, PJ_MAX, PJ_MIN,

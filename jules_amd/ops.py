@@ -191,6 +191,44 @@ def cross_entropy(logits, targets, grad=None, loss=None, workspace=None):
     return loss, grad
 
 
+def mlp_workspace(M, K1, N1, N2, device):
+    nbytes = lib().jules_hip_mlp_workspace_size(int(M), int(K1), int(N1), int(N2))
+    return torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
+
+
+def mlp_forward_backward(X, W1, b1, W2, b2, targets, with_dX=False, workspace=None):
+    """interleavedMLPForwardBackward (InterleavedAutodiff.h:55): fp32 2-layer
+    MLP, softmax cross entropy against int32 targets, and the gradients.
+    Returns a dict with output, loss (1 element), dW1, db1, dW2, db2 and
+    dX (None unless with_dX), all on X's device."""
+    _need(X, "X", (torch.float32,))
+    for t, n in ((W1, "W1"), (b1, "b1"), (W2, "W2"), (b2, "b2")):
+        _need(t, n, (torch.float32,), X.device)
+    _need(targets, "targets", (torch.int32,), X.device)
+    M, K1 = X.shape
+    K1b, N1 = W1.shape
+    N1b, N2 = W2.shape
+    if K1b != K1 or N1b != N1 or b1.numel() != N1 or b2.numel() != N2 or targets.numel() != M:
+        raise ValueError("mlp: operand shapes disagree")
+    dev = X.device
+    out = {
+        "output": torch.empty((M, N2), dtype=torch.float32, device=dev),
+        "loss": torch.empty((1,), dtype=torch.float32, device=dev),
+        "dW1": torch.empty((K1, N1), dtype=torch.float32, device=dev),
+        "db1": torch.empty((N1,), dtype=torch.float32, device=dev),
+        "dW2": torch.empty((N1, N2), dtype=torch.float32, device=dev),
+        "db2": torch.empty((N2,), dtype=torch.float32, device=dev),
+        "dX": torch.empty((M, K1), dtype=torch.float32, device=dev) if with_dX else None,
+    }
+    if workspace is None:
+        workspace = mlp_workspace(M, K1, N1, N2, dev)
+    check(lib().jules_hip_mlp_forward_backward(
+        _ptr(X), _ptr(W1), _ptr(b1), _ptr(W2), _ptr(b2), _ptr(targets), _ptr(out["output"]),
+        _ptr(out["dW1"]), _ptr(out["db1"]), _ptr(out["dW2"]), _ptr(out["db2"]), _ptr(out["dX"]),
+        M, K1, N1, N2, _ptr(out["loss"]), _ptr(workspace), workspace.numel(), _stream(X)))
+    return out
+
+
 def mfma_ceiling(out, workgroups, iters):
     """Launch the MFMA calibration kernel (jules_hip_mfma_ceiling; no
     counterpart in the reference) on torch's current stream: `workgroups` x 4

@@ -125,3 +125,22 @@ def w8a16_inputs(M, N, K, seed=0):
     x = bf16_round(normal(seed, 2, (M, K)))
     bias = uniform(seed, 3, (N,), -0.1, 0.1)
     return x, W, scale, bias
+
+
+def mlp_inputs(M, K1, N1, N2, seed=0, scaled=False):
+    """interleavedMLPForwardBackward operands.  The reference benchmark
+    (benchmarks/bench_kernel.cpp:285-290) draws X, W1, b1, W2, b2 ~ U[-1, 1]
+    and targets ~ U{0..N2-1}; `scaled` divides each weight by sqrt(fan_in) so
+    the logits stay O(1) and the softmax does not saturate."""
+    X = uniform(seed, 0, (M, K1), -1.0, 1.0)
+    W1 = uniform(seed, 1, (K1, N1), -1.0, 1.0)
+    b1 = uniform(seed, 2, (N1,), -1.0, 1.0)
+    W2 = uniform(seed, 3, (N1, N2), -1.0, 1.0)
+    b2 = uniform(seed, 4, (N2,), -1.0, 1.0)
+    if scaled:
+        W1 = (W1 / np.float32(np.sqrt(K1))).astype(np.float32)
+        W2 = (W2 / np.float32(np.sqrt(N1))).astype(np.float32)
+    b = bits(seed, 5, M) >> np.uint64(32)
+    with np.errstate(over="ignore"):
+        t = ((b * np.uint64(N2)) >> np.uint64(32)).astype(np.int32)
+    return X, W1, b1, W2, b2, t

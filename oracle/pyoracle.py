@@ -327,6 +327,47 @@ def cross_entropy64(logits, targets):
     return float(loss), grad
 
 
+def mlp_forward_backward64(X, W1, b1, W2, b2, targets, relu_mask=None):
+    """interleavedMLPForwardBackward (include/jules/Kernel/InterleavedAutodiff.h
+    :55-441) restated in fp64 numpy, whole-matrix instead of per tile (the
+    reference's tiles only change the summation order of its BLAS calls):
+      h = X W1 + b1, a = relu(h)                       :144-166
+      o = a W2 + b2 (the output)                       :168-176
+      p = exp(o - rowmax) / rowsum, loss_i = -log(p[t_i] + 1e-10),
+      dO = (p - onehot(t)) / M                         :178-197
+      dW2 = a^T dO, db2 = colsum(dO)                   :207-221
+      dH = (dO W2^T) * (h > 0)                         :223-247
+      dW1 = X^T dH, db1 = colsum(dH), dX = dH W1^T     :249-267
+      loss = sum_i loss_i / M                          :435
+    Returns a dict of float64 arrays (loss a float).  M = 0 gives zero
+    gradients and a NaN loss (0/0).  relu_mask, if given, replaces h > 0 in
+    the backward (relu'(h) for |h| within rounding of 0 is decided by the
+    rounding of whoever computed h; a checker passes the mask the checked
+    code used)."""
+    X = np.asarray(X, np.float64)
+    W1, b1 = np.asarray(W1, np.float64), np.asarray(b1, np.float64)
+    W2, b2 = np.asarray(W2, np.float64), np.asarray(b2, np.float64)
+    t = np.asarray(targets, np.int64)
+    M = X.shape[0]
+    h = X @ W1 + b1
+    a = np.where(h > 0, h, 0.0)
+    o = a @ W2 + b2
+    if M == 0:
+        z = np.zeros
+        return {"output": o, "loss": float("nan"), "dW1": z(W1.shape), "db1": z(b1.shape),
+                "dW2": z(W2.shape), "db2": z(b2.shape), "dX": z(X.shape)}
+    e = np.exp(o - o.max(axis=1, keepdims=True))
+    p = e / e.sum(axis=1, keepdims=True)
+    rows = np.arange(M)
+    loss = float(np.sum(-np.log(p[rows, t] + 1e-10)) / M)
+    dO = p.copy()
+    dO[rows, t] -= 1.0
+    dO /= M
+    dH = np.where(h > 0 if relu_mask is None else relu_mask, dO @ W2.T, 0.0)
+    return {"output": o, "loss": loss, "dW1": X.T @ dH, "db1": dH.sum(axis=0), "dW2": a.T @ dO,
+            "db2": dO.sum(axis=0), "dX": dH @ W1.T}
+
+
 def max_threads():
     return lib().jo_max_threads()
 

@@ -43,7 +43,8 @@ def test_cxx_shim_symbols_exported():
     text = open(CXX_HEADER).read()
     names = ["fusedMatmulRelu", "fusedMatmulBiasRelu", "tiledMatmulWithActivation", "fusedGelu",
              "matmulInt8", "flashAttention", "attention", "standardAttention", "lastStatus",
-             "fusedSoftmax", "fusedLayerNorm", "fusedCrossEntropyLoss"]
+             "fusedSoftmax", "fusedLayerNorm", "fusedCrossEntropyLoss",
+             "interleavedMLPForwardBackward"]
     for n in names:
         assert re.search(rf"\b{n}\s*\(", text), n
         mangled = f"_ZN5jules6kernel{len(n)}{n}E"
@@ -64,7 +65,7 @@ def test_registry_names():
     routed = ["fusedMatmulRelu", "fusedMatmulSigmoid", "fusedMatmulTanh", "fusedMatmulGelu",
               "fusedMatmulBiasRelu", "fusedMatmulBiasSigmoid", "fusedMatmulBiasTanh",
               "fusedGelu", "matmulInt8", "flashAttention", "fusedSoftmax", "fusedLayerNorm",
-              "fusedCrossEntropyLoss"]
+              "fusedCrossEntropyLoss", "interleavedMLPForwardBackward"]
     added = ["fusedMatmulBiasGelu", "flashAttentionCausal", "matmulW8A16BiasSilu"]
     for n in routed + added:
         assert n in names
@@ -199,3 +200,20 @@ def test_w8a8_validation():
     assert L.jules_hip_matmul_w8a8(16, 16, 16, 4, 4, 4, None, None, None, None) == 1   # scale_B
     assert L.jules_hip_matmul_w8a8(16, 16, 16, 4, 4, 4, 2, 16, None, None) == 4        # scale_A
     assert L.jules_hip_matmul_w8a8(16, 16, 18, 4, 4, 4, None, 16, None, None) == 4      # C
+
+
+def test_mlp_validation():
+    L = _lib.lib()
+    f = L.jules_hip_mlp_forward_backward
+    assert L.jules_hip_mlp_workspace_size(4, 3, 0, 2) == 0
+    assert L.jules_hip_mlp_workspace_size(4, 3, 5, 2) > 0
+    args = [P] * 12 + [4, 3, 5, 2, P, P, 1 << 20, None]
+    bad = list(args)
+    bad[13] = 0  # K1 = 0
+    assert f(*bad) == SHAPE
+    bad = list(args)
+    bad[1] = None  # W1
+    assert f(*bad) == NULL
+    bad = list(args)
+    bad[17] = 0  # workspace bytes
+    assert f(*bad) == WS

@@ -433,3 +433,104 @@ def test_cross_entropy_against_fp64_and_invariants(M, N):
     # uniform logits: loss = log N (up to the 1e-10 guard)
     lu, _ = po.cross_entropy(np.zeros((M, N), np.float32), t)
     assert abs(lu - np.log(N)) < 1e-5 * max(1.0, np.log(N)) + 1e-6
+
+
+# ---- 2-layer MLP forward + backward (interleavedMLPForwardBackward) --------
+def _mlp_loss64(X, W1, b1, W2, b2, t):
+    return po.mlp_forward_backward64(X, W1, b1, W2, b2, t)["loss"]
+
+
+def test_mlp_oracle_gradients_match_finite_differences():
+    """Central differences of the oracle's own loss, in fp64, on a tiny MLP:
+    a dropped term, a transposed product or a wrong mask in any gradient
+    fails.  (The analytic gradient is (p - onehot)/M, the derivative of
+    -log p; the +1e-10 inside the log moves it by ~1e-10/p.)"""
+    X, W1, b1, W2, b2, t = I.mlp_inputs(5, 4, 6, 3, seed=3, scaled=True)
+    X, W1, b1, W2, b2 = (np.asarray(a, np.float64) for a in (X, W1, b1, W2, b2))
+    g = po.mlp_forward_backward64(X, W1, b1, W2, b2, t)
+    params = {"dX": X, "dW1": W1, "db1": b1, "dW2": W2, "db2": b2}
+    eps = 1e-6
+    for name, arr in params.items():
+        num = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            old = arr[idx]
+            arr[idx] = old + eps
+            lp = _mlp_loss64(X, W1, b1, W2, b2, t)
+            arr[idx] = old - eps
+            lm = _mlp_loss64(X, W1, b1, W2, b2, t)
+            arr[idx] = old
+            num[idx] = (lp - lm) / (2 * eps)
+        np.testing.assert_allclose(g[name], num, rtol=1e-6, atol=1e-8, err_msg=name)
+    # an explicit relu mask equal to h > 0 changes nothing; the opposite mask
+    # changes the layer-1 gradients
+    h = X @ W1 + b1
+    same = po.mlp_forward_backward64(X, W1, b1, W2, b2, t, relu_mask=h > 0)
+    flip = po.mlp_forward_backward64(X, W1, b1, W2, b2, t, relu_mask=h <= 0)
+    for name in g:
+        np.testing.assert_array_equal(np.asarray(same[name]), np.asarray(g[name]), err_msg=name)
+    assert not np.allclose(flip["dW1"], g["dW1"]) and np.array_equal(flip["dW2"], g["dW2"])
+
+
+def test_mlp_oracle_against_torch_autograd():
+    """An independent implementation: torch autograd (CPU, fp64) of the same
+    graph, with the loss written as in the reference (:188-194)."""
+    torch = pytest.importorskip("torch")
+    X, W1, b1, W2, b2, t = I.mlp_inputs(37, 20, 33, 10, seed=4, scaled=True)
+    ts = [torch.tensor(np.asarray(a, np.float64), requires_grad=True) for a in (X, W1, b1, W2, b2)]
+    Xt, W1t, b1t, W2t, b2t = ts
+    h = Xt @ W1t + b1t
+    o = torch.relu(h) @ W2t + b2t
+    p = torch.softmax(o, dim=1)
+    loss = -torch.log(p[torch.arange(37), torch.tensor(t, dtype=torch.long)] + 1e-10).sum() / 37
+    loss.backward()
+    g = po.mlp_forward_backward64(X, W1, b1, W2, b2, t)
+    assert abs(g["loss"] - loss.item()) <= 1e-12 * abs(loss.item())
+    np.testing.assert_allclose(g["output"], o.detach().numpy(), rtol=1e-12, atol=1e-12)
+    for name, tt in zip(("dX", "dW1", "db1", "dW2", "db2"), ts):
+        # autograd differentiates the +1e-10 too: relative effect <= 1e-10 / min p
+        np.testing.assert_allclose(g[name], tt.grad.numpy(), rtol=1e-6, atol=1e-9, err_msg=name)
+
+
+def test_mlp_oracle_closed_forms():
+    """W2 = 0: the output is b2 in every row, so dO = (softmax(b2) -
+    onehot(t))/M, db2 is its column sum, and nothing reaches layer 1 (dW1 =
+    db1 = dX = 0).  The loss and dO part must also agree with the C
+    restatement of fusedCrossEntropyLoss on the oracle's output."""
+    X, W1, b1, W2, b2, t = I.mlp_inputs(9, 7, 5, 4, seed=5)
+    W2 = np.zeros_like(W2)
+    g = po.mlp_forward_backward64(X, W1, b1, W2, b2, t)
+    np.testing.assert_allclose(g["output"], np.tile(b2.astype(np.float64), (9, 1)), atol=0)
+    e = np.exp(b2.astype(np.float64) - b2.max())
+    sm = e / e.sum()
+    dO = np.tile(sm, (9, 1))
+    dO[np.arange(9), t] -= 1
+    dO /= 9
+    np.testing.assert_allclose(g["db2"], dO.sum(0), rtol=1e-12, atol=1e-15)
+    for name in ("dW1", "db1", "dX"):
+        assert not np.any(g[name]), name
+    # loss/dO against the C cross-entropy restatement at generic weights
+    X, W1, b1, W2, b2, t = I.mlp_inputs(16, 8, 12, 6, seed=6, scaled=True)
+    g = po.mlp_forward_backward64(X, W1, b1, W2, b2, t)
+    loss_c, grad_c = po.cross_entropy64(g["output"].astype(np.float32), t)
+    assert abs(loss_c - g["loss"]) <= 1e-6 * abs(g["loss"])
+    a = np.maximum(np.asarray(X, np.float64) @ W1 + b1, 0)
+    np.testing.assert_allclose(g["dW2"], a.T @ grad_c, rtol=1e-5, atol=1e-7)
+
+
+def test_mlp_oracle_planted_mistake_is_caught():
+    """A mask taken from the wrong sign (h < 0), planted in a copy of the
+    oracle's backward, gives a db1 that the oracle's (finite-difference
+    checked) db1 rejects."""
+    X, W1, b1, W2, b2, t = I.mlp_inputs(5, 4, 6, 3, seed=3, scaled=True)
+    X, W1, b1, W2, b2 = (np.asarray(a, np.float64) for a in (X, W1, b1, W2, b2))
+    g = po.mlp_forward_backward64(X, W1, b1, W2, b2, t)
+    h = X @ W1 + b1
+    # rebuild dH with the planted sign error and compare db1
+    a = np.where(h > 0, h, 0)
+    o = a @ W2 + b2
+    p = np.exp(o - o.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    p[np.arange(5), t] -= 1
+    p /= 5
+    wrong = np.where(h < 0, p @ W2.T, 0).sum(0)
+    assert not np.allclose(wrong, g["db1"], rtol=1e-3)
