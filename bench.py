@@ -187,8 +187,9 @@ class Runner:
         elif s["kind"] == "xent":
             ops.cross_entropy(self.x, self.t, grad=self.y, loss=self.loss, workspace=self.ws)
         elif s["kind"] == "mlp":
-            ops.mlp_forward_backward(self.X, self.W1, self.b1, self.W2, self.b2, self.t,
-                                     with_dX=True, workspace=self.ws)
+            self.out = ops.mlp_forward_backward(self.X, self.W1, self.b1, self.W2, self.b2, self.t,
+                                                with_dX=True, workspace=self.ws,
+                                                out=getattr(self, "out", None))
         else:
             ops.w8a16_gemm(self.x, self.W[self.i % self.nw], self.scale, self.bias, s["act"],
                            out=self.y, workspace=self.ws)

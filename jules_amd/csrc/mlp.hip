@@ -29,6 +29,8 @@
 // which dimension the global loads run along; the LDS layout is the same.
 // Out-of-range elements are loaded as 0 (any summation order is allowed
 // here: the reference's products are BLAS calls).
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -48,13 +50,15 @@ template <bool TA, bool TB, int EPI>
 __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
     const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
     float* __restrict__ C, int ldc, int M, int N, int K, const float* __restrict__ bias,
-    const float* __restrict__ mask, int ldm) {
+    const float* __restrict__ mask, int ldm, int kc, float* __restrict__ part) {
     __shared__ float As[2][BK * LDA_S];
     __shared__ float Bs[2][BK * LDB_S];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;  // 64x64 quadrant of the tile
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // this workgroup's K range (split-K: blockIdx.z of gridDim.z)
+    const int kb = blockIdx.z * kc, ke = min(K, kb + kc);
 
     float ra[PA], rb[PB];
     // element e of a slice: along the dimension contiguous in memory
@@ -65,7 +69,7 @@ __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
             const int m = TA ? (e & (BM - 1)) : (e >> 4);
             const int k = TA ? (e >> 7) : (e & (BK - 1));
             const int gm = m0 + m, gk = k0 + k;
-            const bool ok = gm < M && gk < K;
+            const bool ok = gm < M && gk < ke;
             const int64_t off = TA ? (int64_t)gk * lda + gm : (int64_t)gm * lda + gk;
             const float v = A[ok ? off : 0];  // branch-free: element 0, then dropped
             ra[p] = ok ? v : 0.0f;
@@ -76,7 +80,7 @@ __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
             const int n = TB ? (e >> 4) : (e & (BN - 1));
             const int k = TB ? (e & (BK - 1)) : (e >> 7);
             const int gn = n0 + n, gk = k0 + k;
-            const bool ok = gn < N && gk < K;
+            const bool ok = gn < N && gk < ke;
             const int64_t off = TB ? (int64_t)gn * ldb + gk : (int64_t)gk * ldb + gn;
             const float v = B[ok ? off : 0];
             rb[p] = ok ? v : 0.0f;
@@ -107,14 +111,14 @@ __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int nk = (K + BK - 1) / BK;
-    gload(0);
+    const int nk = (ke - kb + BK - 1) / BK;
+    gload(kb);
     sstore(0);
     __syncthreads();
     const int lr = lane & 31, lk = lane >> 5;  // MFMA operand: row/col lr, k lk
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
+        if (kt + 1 < nk) gload(kb + (kt + 1) * BK);
         const float* as = As[buf];
         const float* bs = Bs[buf];
 #pragma unroll
@@ -142,6 +146,15 @@ __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
         for (int j = 0; j < 2; ++j) {
             const int n = n0 + wn * 64 + j * 32 + lr;
             if (n >= N) continue;
+            if (part) {  // split-K: raw partial sums, epilogue in the reduction
+                float* pz = part + (int64_t)blockIdx.z * M * N;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                    if (m < M) pz[(int64_t)m * N + n] = acc[i][j][r];
+                }
+                continue;
+            }
             float bn = 0.0f;
             if constexpr (EPI == 1 || EPI == 2) bn = bias[n];
 #pragma unroll
@@ -162,6 +175,28 @@ __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
         }
 }
 
+// Split-K reduction: C = epilogue(sum over z of part[z], in z order).
+template <int EPI>
+__global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
+                                     float* __restrict__ C, int ldc, const float* __restrict__ bias,
+                                     const float* __restrict__ mask, int ldm) {
+    const int64_t total = (int64_t)M * N, stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
+        float v = part[e];
+        for (int z = 1; z < S; ++z) v += part[(int64_t)z * total + e];
+        if constexpr (EPI == 1) {
+            v = v + bias[n];
+        } else if constexpr (EPI == 2) {
+            v = v + bias[n];
+            v = v > 0.0f ? v : 0.0f;
+        } else if constexpr (EPI == 3) {
+            v = mask[(int64_t)m * ldm + n] > 0.0f ? v : 0.0f;
+        }
+        C[(int64_t)m * ldc + n] = v;
+    }
+}
+
 // Column sums in a fixed order: partial[s][n] sums rows [s*R, (s+1)*R) in
 // row order, then out[n] sums the partials in s order.
 __global__ void colsum_partial_kernel(const float* __restrict__ X, int M, int N, int ld, int R,
@@ -171,7 +206,16 @@ __global__ void colsum_partial_kernel(const float* __restrict__ X, int M, int N,
     if (n >= N) return;
     const int r0 = s * R, r1 = min(M, r0 + R);
     float acc = 0.0f;
-    for (int m = r0; m < r1; ++m) acc += X[(int64_t)m * ld + n];
+    int m = r0;
+    // 8 loads in flight, added in row order
+    for (; m + 8 <= r1; m += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = X[(int64_t)(m + u) * ld + n];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; m < r1; ++m) acc += X[(int64_t)m * ld + n];
     part[(int64_t)s * N + n] = acc;
 }
 
@@ -191,12 +235,42 @@ __global__ void fill_kernel(float* __restrict__ p, int64_t n, float v) {
 
 enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RELU = 2, EPI_MASK = 3 };
 
+// Split-K plan: a GEMM with fewer than 128 output tiles gets its K range
+// split (at least 4 slices per split) so that about 256 workgroups run; the
+// partial sums go to the workspace and a reduction applies the epilogue.
+struct KPlan {
+    int S;   // splits
+    int kc;  // K elements per split, a multiple of BK
+};
+
+KPlan kplan(int M, int N, int K) {
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int max_s = K / (4 * BK);
+    if (tiles == 0 || tiles >= 128 || max_s < 2) return {1, K};
+    int S = (256 + tiles - 1) / tiles;
+    if (S > max_s) S = max_s;
+    const int kc = ((K + S - 1) / S + BK - 1) / BK * BK;
+    return {(K + kc - 1) / kc, kc};
+}
+
+size_t kplan_floats(int M, int N, int K) {
+    const KPlan p = kplan(M, N, K);
+    return p.S > 1 ? (size_t)p.S * M * N : 0;
+}
+
 template <bool TA, bool TB, int EPI>
 hipError_t gemm(const float* A, int lda, const float* B, int ldb, float* C, int ldc, int M, int N,
-                int K, const float* bias, const float* mask, int ldm, hipStream_t s) {
-    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+                int K, const float* bias, const float* mask, int ldm, float* part, hipStream_t s) {
+    const KPlan p = kplan(M, N, K);
+    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, p.S);
     hipLaunchKernelGGL((gemm_f32_mfma_kernel<TA, TB, EPI>), grid, dim3(GT), 0, s, A, lda, B, ldb, C,
-                       ldc, M, N, K, bias, mask, ldm);
+                       ldc, M, N, K, bias, mask, ldm, p.kc, p.S > 1 ? part : nullptr);
+    if (p.S > 1) {
+        int64_t b = ((int64_t)M * N + 255) / 256;
+        if (b > 2048) b = 2048;
+        hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3((unsigned)b), dim3(256), 0, s, part, p.S,
+                           M, N, C, ldc, bias, mask, ldm);
+    }
     return hipGetLastError();
 }
 
@@ -239,8 +313,15 @@ size_t mlp_workspace_size(int M, int K1, int N1, int N2) {
     int R;
     const int S = colsum_chunks(M, &R);
     const size_t mn1 = (size_t)M * N1 * sizeof(float), mn2 = (size_t)M * N2 * sizeof(float);
+    // split-K partials of the five products (only skinny ones split)
+    size_t kp = kplan_floats(M, N1, K1);
+    kp = std::max(kp, kplan_floats(M, N2, N1));
+    kp = std::max(kp, kplan_floats(N1, N2, M));
+    kp = std::max(kp, kplan_floats(M, N1, N2));
+    kp = std::max(kp, kplan_floats(K1, N1, M));
+    kp = std::max(kp, kplan_floats(M, K1, N1));
     return 2 * align256(mn1) + align256(mn2) + align256((size_t)M * sizeof(float)) +
-           align256((size_t)S * (N1 > N2 ? N1 : N2) * sizeof(float));
+           align256((size_t)S * (N1 > N2 ? N1 : N2) * sizeof(float)) + align256(kp * sizeof(float));
 }
 
 hipError_t launch_mlp_forward_backward(const float* X, const float* W1, const float* b1,
@@ -266,27 +347,31 @@ hipError_t launch_mlp_forward_backward(const float* X, const float* W1, const fl
     float* dO = reinterpret_cast<float*>(w + 2 * mn1);
     float* row_loss = reinterpret_cast<float*>(w + 2 * mn1 + mn2);
     float* part = reinterpret_cast<float*>(w + 2 * mn1 + mn2 + align256((size_t)M * sizeof(float)));
+    int R;
+    const int S = colsum_chunks(M, &R);
+    float* kpart = reinterpret_cast<float*>(reinterpret_cast<char*>(part) +
+                                            align256((size_t)S * (N1 > N2 ? N1 : N2) * sizeof(float)));
 
     hipError_t e;
     // forward
-    if ((e = gemm<false, false, EPI_BIAS_RELU>(X, K1, W1, N1, act, N1, M, N1, K1, b1, nullptr, 0, s)))
+    if ((e = gemm<false, false, EPI_BIAS_RELU>(X, K1, W1, N1, act, N1, M, N1, K1, b1, nullptr, 0, kpart, s)))
         return e;
-    if ((e = gemm<false, false, EPI_BIAS>(act, N1, W2, N2, output, N2, M, N2, N1, b2, nullptr, 0, s)))
+    if ((e = gemm<false, false, EPI_BIAS>(act, N1, W2, N2, output, N2, M, N2, N1, b2, nullptr, 0, kpart, s)))
         return e;
     // loss and dO
     if ((e = launch_cross_entropy(output, targets, dO, loss, row_loss, M, N2, s))) return e;
     // layer 2 gradients
-    if ((e = gemm<true, false, EPI_NONE>(act, N1, dO, N2, dW2, N2, N1, N2, M, nullptr, nullptr, 0, s)))
+    if ((e = gemm<true, false, EPI_NONE>(act, N1, dO, N2, dW2, N2, N1, N2, M, nullptr, nullptr, 0, kpart, s)))
         return e;
     if ((e = colsum(dO, M, N2, part, db2, s))) return e;
     // dH = (dO W2^T) * (a > 0)
-    if ((e = gemm<false, true, EPI_MASK>(dO, N2, W2, N2, dH, N1, M, N1, N2, nullptr, act, N1, s)))
+    if ((e = gemm<false, true, EPI_MASK>(dO, N2, W2, N2, dH, N1, M, N1, N2, nullptr, act, N1, kpart, s)))
         return e;
     // layer 1 gradients
-    if ((e = gemm<true, false, EPI_NONE>(X, K1, dH, N1, dW1, N1, K1, N1, M, nullptr, nullptr, 0, s)))
+    if ((e = gemm<true, false, EPI_NONE>(X, K1, dH, N1, dW1, N1, K1, N1, M, nullptr, nullptr, 0, kpart, s)))
         return e;
     if ((e = colsum(dH, M, N1, part, db1, s))) return e;
-    if (dX && (e = gemm<false, true, EPI_NONE>(dH, N1, W1, N1, dX, K1, M, K1, N1, nullptr, nullptr, 0, s)))
+    if (dX && (e = gemm<false, true, EPI_NONE>(dH, N1, W1, N1, dX, K1, M, K1, N1, nullptr, nullptr, 0, kpart, s)))
         return e;
     return hipSuccess;
 }

@@ -196,11 +196,12 @@ def mlp_workspace(M, K1, N1, N2, device):
     return torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
 
 
-def mlp_forward_backward(X, W1, b1, W2, b2, targets, with_dX=False, workspace=None):
+def mlp_forward_backward(X, W1, b1, W2, b2, targets, with_dX=False, workspace=None, out=None):
     """interleavedMLPForwardBackward (InterleavedAutodiff.h:55): fp32 2-layer
     MLP, softmax cross entropy against int32 targets, and the gradients.
     Returns a dict with output, loss (1 element), dW1, db1, dW2, db2 and
-    dX (None unless with_dX), all on X's device."""
+    dX (None unless with_dX), all on X's device; `out`, a dict returned by an
+    earlier call with the same shapes, is reused instead of allocating."""
     _need(X, "X", (torch.float32,))
     for t, n in ((W1, "W1"), (b1, "b1"), (W2, "W2"), (b2, "b2")):
         _need(t, n, (torch.float32,), X.device)
@@ -211,15 +212,26 @@ def mlp_forward_backward(X, W1, b1, W2, b2, targets, with_dX=False, workspace=No
     if K1b != K1 or N1b != N1 or b1.numel() != N1 or b2.numel() != N2 or targets.numel() != M:
         raise ValueError("mlp: operand shapes disagree")
     dev = X.device
-    out = {
-        "output": torch.empty((M, N2), dtype=torch.float32, device=dev),
-        "loss": torch.empty((1,), dtype=torch.float32, device=dev),
-        "dW1": torch.empty((K1, N1), dtype=torch.float32, device=dev),
-        "db1": torch.empty((N1,), dtype=torch.float32, device=dev),
-        "dW2": torch.empty((N1, N2), dtype=torch.float32, device=dev),
-        "db2": torch.empty((N2,), dtype=torch.float32, device=dev),
-        "dX": torch.empty((M, K1), dtype=torch.float32, device=dev) if with_dX else None,
-    }
+    if out is not None:
+        with_dX = out["dX"] is not None
+        shapes = {"output": (M, N2), "loss": (1,), "dW1": (K1, N1), "db1": (N1,), "dW2": (N1, N2),
+                  "db2": (N2,), "dX": (M, K1)}
+        for k, shp in shapes.items():
+            if out[k] is None:
+                continue
+            _need(out[k], k, (torch.float32,), dev)
+            if tuple(out[k].shape) != shp or not out[k].is_contiguous():
+                raise ValueError(f"mlp: out[{k!r}] must be a contiguous {shp} tensor")
+    else:
+        out = {
+            "output": torch.empty((M, N2), dtype=torch.float32, device=dev),
+            "loss": torch.empty((1,), dtype=torch.float32, device=dev),
+            "dW1": torch.empty((K1, N1), dtype=torch.float32, device=dev),
+            "db1": torch.empty((N1,), dtype=torch.float32, device=dev),
+            "dW2": torch.empty((N1, N2), dtype=torch.float32, device=dev),
+            "db2": torch.empty((N2,), dtype=torch.float32, device=dev),
+            "dX": torch.empty((M, K1), dtype=torch.float32, device=dev) if with_dX else None,
+        }
     if workspace is None:
         workspace = mlp_workspace(M, K1, N1, N2, dev)
     check(lib().jules_hip_mlp_forward_backward(
