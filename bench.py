@@ -10,7 +10,8 @@ synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 The same run also times every BASELINE config on its own (per_config, keys
 c1-c5), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
 entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
-(per_config, keys m1-m2, fp32 TFLOP/s), the dominant kernel against its roofline
+(per_config, keys m1-m2, fp32 TFLOP/s), the flash-attention backward at C4's
+shape (per_config, key b4), the dominant kernel against its roofline
 (roofline), and the CPU port of the reference AVX-512 path on a bounded
 sample (cpu_baseline).
 
@@ -83,6 +84,14 @@ MLP_CONFIGS = {
 }
 
 
+# Flash-attention backward at C4's shape (training counterpart of the forward;
+# no reference kernel): algorithmic work 2.5x the forward's (dV, dP, dQ, dK
+# and the recomputed S: five products against the forward's two).
+BWD_CONFIGS = {
+    "b4": dict(kind="flash_bwd", dtype="bf16", B=8, H=32, S=4096, D=128, causal=True),
+}
+
+
 def mlp_flops(spec):
     """Forward 2M(K1 N1 + N1 N2); backward dW2, dA, dW1, dX: 2M(N1 N2 + N1 N2
     + K1 N1 + K1 N1)."""
@@ -149,6 +158,17 @@ class Runner:
                 self.ws = ops.cross_entropy_workspace(M, dev)
             self.work = row_bytes(s)
             self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK["hbm"]
+        elif s["kind"] == "flash_bwd":
+            B, H, S, D = s["B"], s["H"], s["S"], s["D"]
+            mk = lambda: torch.randn((B, H, S, D), generator=g, device=dev).bfloat16()
+            self.Q, self.K, self.V, self.dO = mk(), mk(), mk(), mk()
+            self.scale = ops.default_scale(D)
+            self.lse = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+            self.O = ops.flash_attention(self.Q, self.K, self.V, s["causal"], self.scale, lse=self.lse)
+            self.grads = [torch.empty_like(self.Q) for _ in range(3)]
+            self.ws = torch.empty((B * H * S * 4,), dtype=torch.uint8, device=dev)
+            self.work = 2.5 * flash_flops(B, H, S, D, s["causal"])
+            self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK["bf16"]
         elif s["kind"] == "mlp":
             M, K1, N1, N2 = s["M"], s["K1"], s["N1"], s["N2"]
             u = lambda *shape: torch.rand(shape, generator=g, device=dev) * 2 - 1
@@ -186,6 +206,9 @@ class Runner:
             ops.layernorm(self.x, self.gamma, self.beta, out=self.y)
         elif s["kind"] == "xent":
             ops.cross_entropy(self.x, self.t, grad=self.y, loss=self.loss, workspace=self.ws)
+        elif s["kind"] == "flash_bwd":
+            ops.flash_attention_bwd(self.Q, self.K, self.V, self.O, self.dO, self.lse, s["causal"],
+                                    self.scale, *self.grads, workspace=self.ws)
         elif s["kind"] == "mlp":
             self.out = ops.mlp_forward_backward(self.X, self.W1, self.b1, self.W2, self.b2, self.t,
                                                 with_dX=True, workspace=self.ws,
@@ -371,7 +394,7 @@ def main():
 
     # ---- per-config launch timings -----------------------------------------
     per = {}
-    ALL = {**CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS}
+    ALL = {**CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS}
     names = [n for n in ALL if not args.only or n in args.only.split(",")]
     if args.step_only:
         names = []
@@ -379,7 +402,7 @@ def main():
         log(f"config {name} {ALL[name]}")
         try:
             r = Runner(name, ALL[name], dev)
-            iters = 20 if name in ("c3", "c4", "m2") else 50
+            iters = 20 if name in ("c3", "c4", "m2", "b4") else 50
             durs, _ = time_launches([r], 5, iters)
             d = sorted(durs[0])
             med = statistics.median(d)

@@ -127,6 +127,28 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale,
                              void* O, float* lse, int B, int H, int S, int D,
                              void* stream);
 
+/* ---- flash-attention backward --------------------------------------------
+ * Gradients of jules_hip_flash_attn_fwd: with P = exp(scale * Q K^T - lse)
+ * (masked entries 0) and dvec = rowsum(dO * O),
+ *   dV = P^T dO,  dS = P * (dO V^T - dvec),  dQ = scale dS K,  dK = scale dS^T Q.
+ * No reference counterpart: the reference's attention is forward only
+ * (FlashAttention.h:130-309); this is the training path for the forward above.
+ * dtype JH_BF16 (JH_F32 returns JH_ERR_UNSUPPORTED); Q, K, V, O, dO, dQ, dK,
+ * dV [B,H,S,D] of that dtype, 16-byte aligned; lse fp32 [B,H,S] as written by
+ * the forward with the same causal and scale; D 64 or 128.  fp32
+ * accumulation; deterministic (no atomics).
+ * workspace: jules_hip_flash_attn_bwd_workspace_size(B,H,S) bytes (fp32
+ * dvec), 4-byte aligned, no initialisation.
+ */
+size_t jules_hip_flash_attn_bwd_workspace_size(int B, int H, int S);
+int jules_hip_flash_attn_bwd(int dtype, int causal, float scale,
+                             const void* Q, const void* K, const void* V,
+                             const void* O, const void* dO, const float* lse,
+                             void* dQ, void* dK, void* dV,
+                             int B, int H, int S, int D,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* ---- W8A16 decode GEMM + bias + activation --------------------------------
  * y[m,j] = act(scale[j] * sum_k x[m,k] * W[k,j] + bias[j])
  * x bf16 [M,K], W int8 [K,N] (row-major, indexed W[k*N+j] like matmulInt8,

@@ -40,6 +40,9 @@ SIGNATURES = {
     "jules_hip_activation": (_int, [_int, _vp, _vp, _i64, _vp]),
     "jules_hip_flash_attn_fwd": (_int, [_int, _int, _f32, _vp, _vp, _vp, _vp, _vp, _int, _int,
                                         _int, _int, _vp]),
+    "jules_hip_flash_attn_bwd_workspace_size": (_size, [_int, _int, _int]),
+    "jules_hip_flash_attn_bwd": (_int, [_int, _int, _f32] + [_vp] * 9 + [_int] * 4 + [_vp, _size,
+                                                                                  _vp]),
     "jules_hip_w8a16_workspace_size": (_size, [_int, _int, _int]),
     "jules_hip_w8a16_gemm_bias_act": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _int, _int, _int,
                                              _vp, _size, _vp]),

@@ -138,6 +138,38 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale, const void* Q, 
                      "flash launch");
 }
 
+size_t jules_hip_flash_attn_bwd_workspace_size(int B, int H, int S) {
+    if (B < 0 || H < 0 || S < 0) return 0;
+    return jh::flash_bwd_workspace_size(B, H, S);
+}
+
+int jules_hip_flash_attn_bwd(int dtype, int causal, float scale, const void* Q, const void* K,
+                             const void* V, const void* O, const void* dO, const float* lse,
+                             void* dQ, void* dK, void* dV, int B, int H, int S, int D,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+    if (dtype != JH_F32 && dtype != JH_BF16) return fail(JH_ERR_DTYPE, "flash bwd: dtype %d", dtype);
+    if (B < 0 || H < 0 || S < 0) return fail(JH_ERR_SHAPE, "flash bwd: B=%d H=%d S=%d", B, H, S);
+    if (D != 64 && D != 128) return fail(JH_ERR_UNSUPPORTED, "flash bwd: head_dim %d (64 or 128)", D);
+    if (dtype != JH_BF16) return fail(JH_ERR_UNSUPPORTED, "flash bwd: only bf16 is implemented");
+    if (!(std::isfinite(scale) && scale > 0.0f)) return fail(JH_ERR_ARG, "flash bwd: scale %g", scale);
+    if (causal != 0 && causal != 1) return fail(JH_ERR_ARG, "flash bwd: causal must be 0 or 1");
+    if ((int64_t)B * H * S * D > kMaxElems) return fail(JH_ERR_SHAPE, "flash bwd: too large");
+    if (B == 0 || H == 0 || S == 0) return JH_OK;
+    if (!Q || !K || !V || !O || !dO || !lse || !dQ || !dK || !dV)
+        return fail(JH_ERR_NULL, "flash bwd: null operand");
+    const void* t16[] = {Q, K, V, O, dO, dQ, dK, dV};
+    for (const void* q : t16)
+        if (!aligned(q, 16)) return fail(JH_ERR_ALIGN, "flash bwd: tensors must be 16-byte aligned");
+    if (!aligned(lse, 4)) return fail(JH_ERR_ALIGN, "flash bwd: lse alignment");
+    const size_t need = jh::flash_bwd_workspace_size(B, H, S);
+    if (!workspace || workspace_bytes < need)
+        return fail(JH_ERR_WORKSPACE, "flash bwd: workspace %zu bytes, need %zu", workspace_bytes, need);
+    if (!aligned(workspace, 4)) return fail(JH_ERR_ALIGN, "flash bwd: workspace alignment");
+    return check_hip(jh::launch_flash_bwd(dtype, causal, scale, Q, K, V, O, dO, lse, dQ, dK, dV, B,
+                                          H, S, D, workspace, static_cast<hipStream_t>(stream)),
+                     "flash bwd launch");
+}
+
 size_t jules_hip_w8a16_workspace_size(int M, int N, int K) {
     if (M < 1 || M > 16 || N < 16 || N % 16 || K < 8 || K % 8) return 0;
     return jh::w8a16_workspace_size(M, N, K);

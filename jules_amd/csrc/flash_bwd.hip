@@ -1,0 +1,386 @@
+// flash_bwd.hip - flash-attention backward on gfx950 MFMA (bf16).
+//
+// Gradients of O = softmax(scale * Q K^T [causal mask]) V per (batch, head),
+// Q, K, V, O, dO [B,H,S,D] bf16 row-major, D in {64, 128}, given the
+// forward's natural-log row log-sum-exp lse [B,H,S] (jules_hip_flash_attn_fwd):
+//   P   = exp(scale * Q K^T - lse)           (masked entries 0)
+//   dV  = P^T dO
+//   dP  = dO V^T
+//   dS  = P * (dP - rowsum(dO * O))
+//   dQ  = scale * dS K,   dK = scale * dS^T Q
+// The reference has no backward pass (its flashAttention, FlashAttention.h:
+// 130-309, is forward only); this is the training counterpart of the forward
+// kernel in flash_fwd.hip, with the same operand layouts.
+//
+// Three launches, none with atomics, so results are deterministic:
+//   1. dvec = rowsum(dO * O) in fp32 (HBM-bound);
+//   2. dK, dV: a workgroup owns 128 keys (4 waves x 32) and walks the query
+//      blocks of 64 (from the diagonal on, if causal);
+//   3. dQ: a workgroup owns 128 queries (4 waves x 32) and walks the key
+//      blocks of 64 (up to the diagonal, if causal).
+// The dQ pass recomputes P and dP instead of accumulating dQ across key
+// blocks with atomics.
+//
+// MFMA v_mfma_f32_32x32x16_bf16: lane l supplies A[l%32][8(l/32)..+7] and
+// B[8(l/32)..+7][l%32]; the result's register r of lane l is row
+// 8(r/4) + 4(l/32) + r%4, column l%32.  A product over a 16-long k can take
+// any k order, as long as A and B use the same one: results of one product,
+// whose lane holds the 8 rows {4g + 0..3, 8 + 4g + 0..3} of a 16-row step
+// (g = l/32), are fed straight back as the A (dK/dV pass) or B (dQ pass)
+// operand of the next, and the other operand is read in that order with
+// transposing LDS reads (ds_read_b64_tr_b16: a 16-lane group reads 4 rows x
+// 16 columns, lane i receiving column i of the 4 rows).
+//
+//   dK/dV pass (lane = key column):  S = Q K^T, dP = dO V^T;  then
+//     dV += P^T dO and dK += dS^T Q with P, dS as A and dO, Q read transposed.
+//   dQ pass (lane = query column):   S^T = K Q^T, dP^T = V dO^T;  then
+//     dQ^T += K^T dS^T with dS^T as B and K read transposed.
+// Tiles are staged through LDS with 16 bytes of padding per row (row reads
+// then hit 16 distinct bank groups).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace jh {
+namespace {
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int BW = 4;            // waves per workgroup
+constexpr int BT = BW * 64;      // threads per workgroup
+constexpr int BOWN = BW * 32;    // keys (dK/dV pass) or queries (dQ pass) a workgroup owns
+constexpr int BSTEP = 64;        // query (dK/dV) or key (dQ) rows per loop step
+
+template <int D>
+struct BwdCfg {
+    static constexpr int PITCH = D * 2 + 16;   // bytes per LDS row
+    static constexpr int KS = D / 16;          // 16-wide k steps over the head dim
+    static constexpr int DT = D / 32;          // 32-wide d blocks
+};
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// 8 fp32 -> bf16x8 (round to nearest even)
+__device__ __forceinline__ bf16x8_t pack8(const float* f) {
+    u32x4_t u;
+    u[0] = pack_bf16x2(f[0], f[1]);
+    u[1] = pack_bf16x2(f[2], f[3]);
+    u[2] = pack_bf16x2(f[4], f[5]);
+    u[3] = pack_bf16x2(f[6], f[7]);
+    return __builtin_bit_cast(bf16x8_t, u);
+}
+
+// Copy rows [r0, r0 + nrows) of a [S][D] bf16 matrix into an LDS tile with
+// the padded pitch; rows past S are copies of row S-1 (their results are
+// masked or never stored).
+template <int D>
+__device__ __forceinline__ void load_tile(uint8_t* tile, const uint16_t* __restrict__ src, int r0,
+                                          int nrows, int S, int tid) {
+    constexpr int UNITS = D / 8;  // 16-byte units per row
+    for (int e = tid; e < nrows * UNITS; e += BT) {
+        const int r = e / UNITS, u = e % UNITS;
+        const int gr = min(r0 + r, S - 1);
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(src + (int64_t)gr * D + 8 * u);
+        *reinterpret_cast<u32x4_t*>(tile + r * BwdCfg<D>::PITCH + 16 * u) = v;
+    }
+}
+
+// A/B fragment: 8 consecutive head-dim elements of one row (16 bytes)
+template <int D>
+__device__ __forceinline__ bf16x8_t row_frag(const uint8_t* tile, int row, int ks, int g) {
+    return as_bf16x8(*reinterpret_cast<const u32x4_t*>(tile + row * BwdCfg<D>::PITCH +
+                                                       (16 * ks + 8 * g) * 2));
+}
+
+// Transposed fragment: column (32 dt + lane%32) of the 8 rows
+// {rb + 4g + 0..3, rb + 8 + 4g + 0..3} of a [rows][D] tile.
+template <int D>
+__device__ __forceinline__ bf16x8_t tr_frag(const uint8_t* tile, int rb, int dt, int lane) {
+    const int g = lane >> 5, vs = lane & 15, vdh = (lane >> 4) & 1;
+    const int r = rb + 4 * g + (vs >> 2);
+    const int chunk = 8 * dt + 4 * vdh + (vs & 3);  // 8-byte chunk of the row
+    const uint8_t* p = tile + r * BwdCfg<D>::PITCH + chunk * 8;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * BwdCfg<D>::PITCH));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    const i16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16_t zero16() {
+    f32x16_t z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+    return z;
+}
+
+// ---- 1. dvec = rowsum(dO * O): 16 lanes per row, 16 bytes each -------------
+template <int D>
+__global__ __launch_bounds__(256) void flash_bwd_dvec_kernel(const uint16_t* __restrict__ O,
+                                                             const uint16_t* __restrict__ dO,
+                                                             float* __restrict__ dvec, int64_t rows) {
+    constexpr int LPR = D / 8;  // lanes per row
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t row = t / LPR;
+    const int u = (int)(t % LPR);
+    float s = 0.0f;
+    if (row < rows) {
+        const u32x4_t o = *reinterpret_cast<const u32x4_t*>(O + row * D + 8 * u);
+        const u32x4_t d = *reinterpret_cast<const u32x4_t*>(dO + row * D + 8 * u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s = fmaf(bf16_lo(o[i]), bf16_lo(d[i]), s);
+            s = fmaf(bf16_hi(o[i]), bf16_hi(d[i]), s);
+        }
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (row < rows && u == 0) dvec[row] = s;
+}
+
+// ---- 2. dK, dV ----------------------------------------------------------------
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(BT, 1) void flash_bwd_dkdv_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dvec,
+    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int S, float scale) {
+    using C = BwdCfg<D>;
+    __shared__ __attribute__((aligned(16))) uint8_t k_t[BOWN * C::PITCH];
+    __shared__ __attribute__((aligned(16))) uint8_t v_t[BOWN * C::PITCH];
+    __shared__ __attribute__((aligned(16))) uint8_t q_t[BSTEP * C::PITCH];
+    __shared__ __attribute__((aligned(16))) uint8_t do_t[BSTEP * C::PITCH];
+    __shared__ __attribute__((aligned(16))) float lse_t[BSTEP];
+    __shared__ __attribute__((aligned(16))) float dv_t[BSTEP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 5, col = lane & 31;
+    const int nkb = (S + BOWN - 1) / BOWN;
+    const int bh = blockIdx.x / nkb;
+    const int k0 = (blockIdx.x % nkb) * BOWN;  // longest causal range (first keys) first
+    const int64_t hoff = (int64_t)bh * S * D;
+    const float c = scale * kLog2e;
+
+    load_tile<D>(k_t, K + hoff, k0, BOWN, S, tid);
+    load_tile<D>(v_t, V + hoff, k0, BOWN, S, tid);
+
+    f32x16_t dk[C::DT], dv[C::DT];
+#pragma unroll
+    for (int i = 0; i < C::DT; ++i) {
+        dk[i] = zero16();
+        dv[i] = zero16();
+    }
+    const int krow = wave * 32 + col;  // this lane's key within the tile (S/dP column)
+    const int key = k0 + krow;
+
+    const int qb_begin = CAUSAL ? (k0 / BSTEP) : 0;
+    const int qb_end = (S + BSTEP - 1) / BSTEP;
+    for (int qb = qb_begin; qb < qb_end; ++qb) {
+        const int q0 = qb * BSTEP;
+        __syncthreads();  // previous step's reads of q_t / do_t are done
+        load_tile<D>(q_t, Q + hoff, q0, BSTEP, S, tid);
+        load_tile<D>(do_t, dO + hoff, q0, BSTEP, S, tid);
+        if (tid < BSTEP) {
+            const int q = min(q0 + tid, S - 1);
+            lse_t[tid] = lse[(int64_t)bh * S + q] * kLog2e;
+            dv_t[tid] = dvec[(int64_t)bh * S + q];
+        }
+        __syncthreads();
+
+        // S = Q K^T and dP = dO V^T for the 64 queries x this wave's 32 keys
+        bf16x8_t pa[2][2], sa[2][2];  // P and dS as A operands: [32-query half][16-query step]
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+            for (int ks = 0; ks < C::KS; ++ks) {
+                const bf16x8_t kf = row_frag<D>(k_t, krow, ks, g);
+                const bf16x8_t vf = row_frag<D>(v_t, krow, ks, g);
+                s = mfma(row_frag<D>(q_t, h * 32 + col, ks, g), kf, s);
+                dp = mfma(row_frag<D>(do_t, h * 32 + col, ks, g), vf, dp);
+            }
+            // register r: query h*32 + 8(r/4) + 4g + r%4 of this step
+            float p[16], ds[16];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int ql = h * 32 + 8 * r4 + 4 * g;
+                const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&lse_t[ql]);
+                const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&dv_t[ql]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * r4 + i, q = q0 + ql + i;
+                    const bool live = q < S && (!CAUSAL || key <= q);
+                    const float pv = live ? exp2f(s[r] * c - l4[i]) : 0.0f;
+                    p[r] = pv;
+                    ds[r] = pv * (dp[r] - d4[i]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                pa[h][t] = pack8(p + 8 * t);
+                sa[h][t] = pack8(ds + 8 * t);
+            }
+        }
+        // dV += P^T dO, dK += dS^T Q: A = P / dS (this lane's key), B read
+        // transposed in the matching query order
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int rb = h * 32 + 16 * t;
+                    dv[dt] = mfma(pa[h][t], tr_frag<D>(do_t, rb, dt, lane), dv[dt]);
+                    dk[dt] = mfma(sa[h][t], tr_frag<D>(q_t, rb, dt, lane), dk[dt]);
+                }
+    }
+
+    // dK = scale * dS^T Q, dV = P^T dO; register r of block dt: key row
+    // 8(r/4) + 4g + r%4 of this wave's 32, head dim 32 dt + col
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int kr = k0 + wave * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (kr >= S) continue;
+            const int64_t o = hoff + (int64_t)kr * D + 32 * dt + col;
+            dK[o] = __builtin_bit_cast(uint16_t, (__bf16)(dk[dt][r] * scale));
+            dV[o] = __builtin_bit_cast(uint16_t, (__bf16)dv[dt][r]);
+        }
+}
+
+// ---- 3. dQ ----------------------------------------------------------------------
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(BT, 1) void flash_bwd_dq_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dvec,
+    uint16_t* __restrict__ dQ, int S, float scale) {
+    using C = BwdCfg<D>;
+    __shared__ __attribute__((aligned(16))) uint8_t k_t[BSTEP * C::PITCH];
+    __shared__ __attribute__((aligned(16))) uint8_t v_t[BSTEP * C::PITCH];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 5, col = lane & 31;
+    const int nqb = (S + BOWN - 1) / BOWN;
+    const int bh = blockIdx.x / nqb;
+    const int q0 = (nqb - 1 - blockIdx.x % nqb) * BOWN;  // longest causal range first
+    const int64_t hoff = (int64_t)bh * S * D;
+    const float c = scale * kLog2e;
+
+    // this lane's query (S^T / dP^T column) and its Q, dO fragments (B operands)
+    const int q = q0 + wave * 32 + col;
+    const int qr = min(q, S - 1);
+    bf16x8_t qf[C::KS], of[C::KS];
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+        qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(Q + hoff + (int64_t)qr * D + 16 * ks + 8 * g));
+        of[ks] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(dO + hoff + (int64_t)qr * D + 16 * ks + 8 * g));
+    }
+    const float lse2 = lse[(int64_t)bh * S + qr] * kLog2e;
+    const float dvq = dvec[(int64_t)bh * S + qr];
+
+    f32x16_t dq[C::DT];
+#pragma unroll
+    for (int i = 0; i < C::DT; ++i) dq[i] = zero16();
+
+    const int kv_end = CAUSAL ? min(S, q0 + BOWN) : S;
+    for (int kb = 0; kb < kv_end; kb += BSTEP) {
+        __syncthreads();
+        load_tile<D>(k_t, K + hoff, kb, BSTEP, S, tid);
+        load_tile<D>(v_t, V + hoff, kb, BSTEP, S, tid);
+        __syncthreads();
+        // S^T = K Q^T, dP^T = V dO^T: 64 keys x this wave's 32 queries
+        bf16x8_t sb[2][2];  // dS^T as B operands: [32-key half][16-key step]
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+            for (int ks = 0; ks < C::KS; ++ks) {
+                s = mfma(row_frag<D>(k_t, h * 32 + col, ks, g), qf[ks], s);
+                dp = mfma(row_frag<D>(v_t, h * 32 + col, ks, g), of[ks], dp);
+            }
+            // register r: key kb + h*32 + 8(r/4) + 4g + r%4
+            float ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int k = kb + h * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                const bool live = k < S && q < S && (!CAUSAL || k <= q);
+                const float pv = live ? exp2f(s[r] * c - lse2) : 0.0f;
+                ds[r] = pv * (dp[r] - dvq);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) sb[h][t] = pack8(ds + 8 * t);
+        }
+        // dQ^T += K^T dS^T: A = K read transposed in the matching key order
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    dq[dt] = mfma(tr_frag<D>(k_t, h * 32 + 16 * t, dt, lane), sb[h][t], dq[dt]);
+    }
+
+    // dQ = scale * dS K; register r of block dt: head dim 32 dt + 8(r/4) +
+    // 4g + r%4 of this lane's query: 4 consecutive d per 8-byte store
+    if (q >= S) return;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int d = 32 * dt + 8 * r4 + 4 * g;
+            u32x2_t o;
+            o[0] = pack_bf16x2(dq[dt][4 * r4] * scale, dq[dt][4 * r4 + 1] * scale);
+            o[1] = pack_bf16x2(dq[dt][4 * r4 + 2] * scale, dq[dt][4 * r4 + 3] * scale);
+            *reinterpret_cast<u32x2_t*>(dQ + hoff + (int64_t)q * D + d) = o;
+        }
+}
+
+template <int D, bool CAUSAL>
+hipError_t launch_bwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, const uint16_t* O,
+                      const uint16_t* dO, const float* lse, uint16_t* dQ, uint16_t* dK,
+                      uint16_t* dV, int BH, int S, float scale, float* dvec, hipStream_t s) {
+    const int64_t rows = (int64_t)BH * S;
+    const int64_t threads = rows * (D / 8);
+    hipLaunchKernelGGL(flash_bwd_dvec_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       s, O, dO, dvec, rows);
+    const int nb = (S + BOWN - 1) / BOWN;
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, CAUSAL>), dim3(BH * nb), dim3(BT), 0, s, Q, K, V, dO,
+                       lse, dvec, dK, dV, S, scale);
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, CAUSAL>), dim3(BH * nb), dim3(BT), 0, s, Q, K, V, dO,
+                       lse, dvec, dQ, S, scale);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t flash_bwd_workspace_size(int B, int H, int S) { return (size_t)B * H * S * sizeof(float); }
+
+hipError_t launch_flash_bwd(int dtype, int causal, float scale, const void* Q, const void* K,
+                            const void* V, const void* O, const void* dO, const float* lse,
+                            void* dQ, void* dK, void* dV, int B, int H, int S, int D, void* ws,
+                            hipStream_t s) {
+    if (dtype != JH_BF16) return hipErrorInvalidValue;
+    const auto* q = static_cast<const uint16_t*>(Q);
+    const auto* k = static_cast<const uint16_t*>(K);
+    const auto* v = static_cast<const uint16_t*>(V);
+    const auto* o = static_cast<const uint16_t*>(O);
+    const auto* dout = static_cast<const uint16_t*>(dO);
+    auto* dq = static_cast<uint16_t*>(dQ);
+    auto* dk = static_cast<uint16_t*>(dK);
+    auto* dv = static_cast<uint16_t*>(dV);
+    float* dvec = static_cast<float*>(ws);
+    const int BH = B * H;
+    if (D == 128) {
+        return causal ? launch_bwd<128, true>(q, k, v, o, dout, lse, dq, dk, dv, BH, S, scale, dvec, s)
+                      : launch_bwd<128, false>(q, k, v, o, dout, lse, dq, dk, dv, BH, S, scale, dvec, s);
+    }
+    return causal ? launch_bwd<64, true>(q, k, v, o, dout, lse, dq, dk, dv, BH, S, scale, dvec, s)
+                  : launch_bwd<64, false>(q, k, v, o, dout, lse, dq, dk, dv, BH, S, scale, dvec, s);
+}
+
+}  // namespace jh

@@ -16,6 +16,12 @@ hipError_t launch_activation(int act, float* out, const float* in, int64_t n, hi
 hipError_t launch_flash_fwd(int dtype, int causal, float scale, const void* Q, const void* K,
                             const void* V, void* O, float* lse, int B, int H, int S, int D,
                             hipStream_t s);
+// flash-attention backward (flash_bwd.hip): bf16; workspace = fp32 [B,H,S]
+size_t flash_bwd_workspace_size(int B, int H, int S);
+hipError_t launch_flash_bwd(int dtype, int causal, float scale, const void* Q, const void* K,
+                            const void* V, const void* O, const void* dO, const float* lse,
+                            void* dQ, void* dK, void* dV, int B, int H, int S, int D, void* ws,
+                            hipStream_t s);
 size_t w8a16_workspace_size(int M, int N, int K);
 hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float* scale,
                         const float* bias, uint16_t* y, int M, int N, int K, void* ws,

@@ -101,6 +101,39 @@ def flash_attention(Q, K, V, causal=False, scale=None, out=None, lse=None):
     return out
 
 
+def flash_attention_bwd(Q, K, V, O, dO, lse, causal=False, scale=None, dQ=None, dK=None, dV=None,
+                        workspace=None):
+    """Flash-attention backward (jules_hip_flash_attn_bwd; no reference
+    counterpart): (dQ, dK, dV) for the forward O = flash_attention(Q, K, V,
+    causal, scale, lse=lse).  bf16 [B,H,S,D]; lse fp32 [B,H,S]."""
+    _need(Q, "Q", (torch.bfloat16,))
+    for t, n in ((K, "K"), (V, "V"), (O, "O"), (dO, "dO")):
+        _need(t, n, (Q.dtype,), Q.device)
+        if t.shape != Q.shape:
+            raise ValueError(f"{n} must have Q's [B,H,S,D] shape")
+    B, H, S, D = Q.shape
+    _need(lse, "lse", (torch.float32,), Q.device)
+    if lse.numel() != B * H * S:
+        raise ValueError("lse must hold B*H*S floats")
+    if scale is None:
+        scale = default_scale(D)
+    dQ = torch.empty_like(Q) if dQ is None else dQ
+    dK = torch.empty_like(Q) if dK is None else dK
+    dV = torch.empty_like(Q) if dV is None else dV
+    for t, n in ((dQ, "dQ"), (dK, "dK"), (dV, "dV")):
+        _need(t, n, (Q.dtype,), Q.device)
+        if t.shape != Q.shape:
+            raise ValueError(f"{n} must have Q's shape")
+    if workspace is None:
+        nbytes = lib().jules_hip_flash_attn_bwd_workspace_size(B, H, S)
+        workspace = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=Q.device)
+    check(lib().jules_hip_flash_attn_bwd(_DT[Q.dtype], int(bool(causal)), float(scale), _ptr(Q),
+                                         _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse), _ptr(dQ),
+                                         _ptr(dK), _ptr(dV), B, H, S, D, _ptr(workspace),
+                                         workspace.numel(), _stream(Q)))
+    return dQ, dK, dV
+
+
 def w8a16_workspace(M, N, K, device):
     n = lib().jules_hip_w8a16_workspace_size(M, N, K)
     return torch.zeros(max(n, 16), dtype=torch.uint8, device=device)

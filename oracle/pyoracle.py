@@ -327,6 +327,31 @@ def cross_entropy64(logits, targets):
     return float(loss), grad
 
 
+def attention_bwd64(Q, K, V, dO, causal, scale):
+    """Attention backward in fp64 numpy, per (b, h), from the textbook
+    definitions (the reference has no backward; its forward is
+    FlashAttention.h:130-309):
+      S = scale Q K^T (causal: key j > query i masked), P = softmax(S),
+      O = P V, dP = dO V^T, dS = P * (dP - rowsum(dO * O)),
+      dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO.
+    Q, K, V, dO: [B, H, S, D].  Returns (dQ, dK, dV, O) as float64."""
+    Q, K, V, dO = (np.asarray(a, np.float64) for a in (Q, K, V, dO))
+    Sq = Q.shape[2]
+    s = np.einsum("bhid,bhjd->bhij", Q, K) * scale
+    if causal:
+        s = np.where(np.tril(np.ones((Sq, Sq), bool)), s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    O = np.einsum("bhij,bhjd->bhid", p, V)
+    dP = np.einsum("bhid,bhjd->bhij", dO, V)
+    dS = p * (dP - np.sum(dO * O, axis=-1, keepdims=True))
+    dQ = scale * np.einsum("bhij,bhjd->bhid", dS, K)
+    dK = scale * np.einsum("bhij,bhid->bhjd", dS, Q)
+    dV = np.einsum("bhij,bhid->bhjd", p, dO)
+    return dQ, dK, dV, O
+
+
 def mlp_forward_backward64(X, W1, b1, W2, b2, targets, relu_mask=None):
     """interleavedMLPForwardBackward (include/jules/Kernel/InterleavedAutodiff.h
     :55-441) restated in fp64 numpy, whole-matrix instead of per tile (the

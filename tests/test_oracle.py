@@ -534,3 +534,48 @@ def test_mlp_oracle_planted_mistake_is_caught():
     p /= 5
     wrong = np.where(h < 0, p @ W2.T, 0).sum(0)
     assert not np.allclose(wrong, g["db1"], rtol=1e-3)
+
+
+# ---- attention backward ------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_bwd_oracle_finite_differences(causal):
+    """Central differences of L = sum(O * dO) with respect to Q, K and V, in
+    fp64, on a tiny head: a wrong sign, a missing rowsum term, a transposed
+    product or the scale on the wrong gradient fails."""
+    rng = np.random.default_rng(7)
+    Q, K, V, dO = (rng.standard_normal((1, 2, 5, 3)) for _ in range(4))
+    scale = 0.7
+    dQ, dK, dV, _ = po.attention_bwd64(Q, K, V, dO, causal, scale)
+
+    def loss():
+        return float(np.sum(po.attention_bwd64(Q, K, V, dO, causal, scale)[3] * dO))
+
+    eps = 1e-6
+    for name, arr, grad in (("dQ", Q, dQ), ("dK", K, dK), ("dV", V, dV)):
+        num = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            old = arr[idx]
+            arr[idx] = old + eps
+            lp = loss()
+            arr[idx] = old - eps
+            lm = loss()
+            arr[idx] = old
+            num[idx] = (lp - lm) / (2 * eps)
+        np.testing.assert_allclose(grad, num, rtol=1e-6, atol=1e-9, err_msg=name)
+
+
+def test_attention_bwd_oracle_against_torch_autograd():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(8)
+    Q, K, V, dO = (rng.standard_normal((2, 2, 9, 4)) for _ in range(4))
+    for causal in (False, True):
+        ts = [torch.tensor(a, requires_grad=True) for a in (Q, K, V)]
+        s = ts[0] @ ts[1].transpose(-1, -2) * 0.5
+        if causal:
+            s = s.masked_fill(torch.triu(torch.ones(9, 9, dtype=torch.bool), 1), float("-inf"))
+        O = torch.softmax(s, dim=-1) @ ts[2]
+        (O * torch.tensor(dO)).sum().backward()
+        got = po.attention_bwd64(Q, K, V, dO, causal, 0.5)
+        np.testing.assert_allclose(got[3], O.detach().numpy(), rtol=1e-12, atol=1e-12)
+        for g, t in zip(got[:3], ts):
+            np.testing.assert_allclose(g, t.grad.numpy(), rtol=1e-10, atol=1e-12)
