@@ -108,6 +108,103 @@ __device__ __forceinline__ bf16x8_t tr_frag(const uint8_t* tile, int rb, int dt,
     return __builtin_bit_cast(bf16x8_t, v);
 }
 
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// The same transposed fragment by inline asm with an explicit wait
+// (tr_issue / tr_wait): the compiler then keeps the issue order, so reads run
+// ahead of the MFMAs that consume them.  LDS reads complete in order, so a
+// wait for at most N outstanding reads covers every read issued N or more
+// reads earlier.
+template <int D>
+__device__ __forceinline__ uint32_t tr_addr(const uint8_t* tile, int rb, int dt, int lane) {
+    const int g = lane >> 5, vs = lane & 15, vdh = (lane >> 4) & 1;
+    const int r = rb + 4 * g + (vs >> 2);
+    const int chunk = 8 * dt + 4 * vdh + (vs & 3);
+    return (uint32_t)(uintptr_t)(tile + r * BwdCfg<D>::PITCH + chunk * 8);
+}
+struct TrFrag {
+    u32x2_t lo, hi;
+};
+template <int D>
+__device__ __forceinline__ TrFrag tr_issue(uint32_t addr) {
+    TrFrag f;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(f.lo) : "v"(addr) : "memory");
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                 : "=v"(f.hi)
+                 : "v"(addr), "n"(8 * BwdCfg<D>::PITCH)
+                 : "memory");
+    return f;
+}
+template <int N>
+__device__ __forceinline__ bf16x8_t tr_wait(TrFrag& f) {
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(f.lo), "+v"(f.hi) : "n"(N) : "memory");
+    const u32x4_t v = {f.lo[0], f.lo[1], f.hi[0], f.hi[1]};
+    return as_bf16x8(v);
+}
+
+// Runs NM MFMAs whose fragments come from transposing reads: the reads of
+// MFMAs m+1 .. m+L are in flight while m runs, in a ring of L+2 fragments
+// (a fragment is refilled only after the MFMA two before has taken it).
+// addr(m) gives MFMA m's read address, use(m, frag) issues MFMA m.
+template <int D, int NM, int L, typename A, typename U>
+__device__ __forceinline__ void tr_pipeline(A&& addr, U&& use) {
+    constexpr int R = L + 2;
+    TrFrag ring[R];
+    static_for<0, L>([&](auto mi) { ring[decltype(mi)::value] = tr_issue<D>(addr(decltype(mi)::value)); });
+    static_for<0, NM>([&](auto mi) {
+        constexpr int m = decltype(mi)::value;
+        if constexpr (m + L < NM) ring[(m + L) % R] = tr_issue<D>(addr(m + L));
+        constexpr int later = (m + L < NM ? L : NM - 1 - m);  // MFMAs whose reads follow m's
+        use(mi, tr_wait<2 * later>(ring[m % R]));
+    });
+}
+
+// Row fragments (16-byte reads) in the same way: MFMA m takes RPM reads,
+// addr(m, j) is the address of its read j, use(m, frags) issues it.
+__device__ __forceinline__ u32x4_t b128_issue(uint32_t addr) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+template <int N>
+__device__ __forceinline__ void b128_wait(u32x4_t& a) {
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void b128_wait(u32x4_t& a, u32x4_t& b) {
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+template <int NM, int RPM, int L, typename A, typename U>
+__device__ __forceinline__ void row_pipeline(A&& addr, U&& use) {
+    static_assert(RPM == 1 || RPM == 2, "one or two reads per MFMA");
+    constexpr int R = L + 2;
+    u32x4_t ring[R][RPM];
+    auto issue = [&](int m, int slot) {
+#pragma unroll
+        for (int j = 0; j < RPM; ++j) ring[slot][j] = b128_issue(addr(m, j));
+    };
+    static_for<0, L>([&](auto mi) { issue(decltype(mi)::value, decltype(mi)::value); });
+    static_for<0, NM>([&](auto mi) {
+        constexpr int m = decltype(mi)::value;
+        if constexpr (m + L < NM) issue(m + L, (m + L) % R);
+        constexpr int later = (m + L < NM ? L : NM - 1 - m);
+        if constexpr (RPM == 1) b128_wait<later>(ring[m % R][0]);
+        else b128_wait<2 * later>(ring[m % R][0], ring[m % R][1]);
+        use(mi, ring[m % R]);
+    });
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t row_addr(const uint8_t* tile, int row, int ks, int g) {
+    return (uint32_t)(uintptr_t)(tile + row * BwdCfg<D>::PITCH + (16 * ks + 8 * g) * 2);
+}
+
 __device__ __forceinline__ f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -144,18 +241,25 @@ __global__ __launch_bounds__(256) void flash_bwd_dvec_kernel(const uint16_t* __r
 }
 
 // ---- 2. dK, dV ----------------------------------------------------------------
+// 4 waves x 32 keys.  Each wave holds its keys' K rows (the B operand of S)
+// in registers next to the dK/dV accumulators; the V rows (B of dP) are read
+// from an LDS copy of the workgroup's 128 V rows.  With 32-query steps this
+// fits in 256 registers, so two workgroups share a CU (two waves per SIMD).  Q/dO tiles of 32 queries
+// are double buffered in LDS: the global loads of block i+1 are issued into
+// registers before block i is multiplied and stored to the other buffer
+// after, one barrier per block.
+constexpr int KVSTEP = 32;  // queries per dK/dV loop step
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(BT, 1) void flash_bwd_dkdv_kernel(
+__global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dvec,
     uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int S, float scale) {
     using C = BwdCfg<D>;
-    __shared__ __attribute__((aligned(16))) uint8_t k_t[BOWN * C::PITCH];
+    constexpr int UNITS = D / 8;
+    constexpr int PF = 2 * KVSTEP * UNITS / BT;  // prefetched units per thread (Q then dO)
+    __shared__ __attribute__((aligned(16))) uint8_t qo_t[2][2][KVSTEP * C::PITCH];  // [buf][Q, dO]
+    __shared__ __attribute__((aligned(16))) float ld_t[2][2][KVSTEP];               // [buf][lse, dvec]
     __shared__ __attribute__((aligned(16))) uint8_t v_t[BOWN * C::PITCH];
-    __shared__ __attribute__((aligned(16))) uint8_t q_t[BSTEP * C::PITCH];
-    __shared__ __attribute__((aligned(16))) uint8_t do_t[BSTEP * C::PITCH];
-    __shared__ __attribute__((aligned(16))) float lse_t[BSTEP];
-    __shared__ __attribute__((aligned(16))) float dv_t[BSTEP];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
@@ -163,10 +267,44 @@ __global__ __launch_bounds__(BT, 1) void flash_bwd_dkdv_kernel(
     const int bh = blockIdx.x / nkb;
     const int k0 = (blockIdx.x % nkb) * BOWN;  // longest causal range (first keys) first
     const int64_t hoff = (int64_t)bh * S * D;
+    const uint16_t* Qh = Q + hoff;
+    const uint16_t* Oh = dO + hoff;
     const float c = scale * kLog2e;
 
-    load_tile<D>(k_t, K + hoff, k0, BOWN, S, tid);
-    load_tile<D>(v_t, V + hoff, k0, BOWN, S, tid);
+    // this lane's key (S / dP column) and its K row (B operand of S)
+    const int key = k0 + wave * 32 + col;
+    const int kr = min(key, S - 1);
+    bf16x8_t kf[C::KS];
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks)
+        kf[ks] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(K + hoff + (int64_t)kr * D + 16 * ks + 8 * g));
+    load_tile<D>(v_t, V + hoff, k0, BOWN, S, tid);  // made visible by the first barrier
+    const int vrow = wave * 32 + col;
+
+    u32x4_t pf[PF];
+    float pl = 0.0f;
+    auto gload = [&](int q0) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int e = tid + BT * p;
+            const int r = (e / UNITS) % KVSTEP, u = e % UNITS;
+            const int64_t gr = min(q0 + r, S - 1);
+            pf[p] = *reinterpret_cast<const u32x4_t*>((e / UNITS < KVSTEP ? Qh : Oh) + gr * D + 8 * u);
+        }
+        if (tid < 2 * KVSTEP) {
+            const int64_t q = (int64_t)bh * S + min(q0 + (tid % KVSTEP), S - 1);
+            pl = tid < KVSTEP ? lse[q] * kLog2e : dvec[q];
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int e = tid + BT * p;
+            const int r = (e / UNITS) % KVSTEP, u = e % UNITS;
+            *reinterpret_cast<u32x4_t*>(&qo_t[buf][e / UNITS / KVSTEP][r * C::PITCH + 16 * u]) = pf[p];
+        }
+        if (tid < 2 * KVSTEP) ld_t[buf][tid / KVSTEP][tid % KVSTEP] = pl;
+    };
 
     f32x16_t dk[C::DT], dv[C::DT];
 #pragma unroll
@@ -174,36 +312,33 @@ __global__ __launch_bounds__(BT, 1) void flash_bwd_dkdv_kernel(
         dk[i] = zero16();
         dv[i] = zero16();
     }
-    const int krow = wave * 32 + col;  // this lane's key within the tile (S/dP column)
-    const int key = k0 + krow;
 
-    const int qb_begin = CAUSAL ? (k0 / BSTEP) : 0;
-    const int qb_end = (S + BSTEP - 1) / BSTEP;
+    const int qb_begin = CAUSAL ? (k0 / KVSTEP) : 0;
+    const int qb_end = (S + KVSTEP - 1) / KVSTEP;
+    gload(qb_begin * KVSTEP);
+    sstore(0);
+    __syncthreads();
     for (int qb = qb_begin; qb < qb_end; ++qb) {
-        const int q0 = qb * BSTEP;
-        __syncthreads();  // previous step's reads of q_t / do_t are done
-        load_tile<D>(q_t, Q + hoff, q0, BSTEP, S, tid);
-        load_tile<D>(do_t, dO + hoff, q0, BSTEP, S, tid);
-        if (tid < BSTEP) {
-            const int q = min(q0 + tid, S - 1);
-            lse_t[tid] = lse[(int64_t)bh * S + q] * kLog2e;
-            dv_t[tid] = dvec[(int64_t)bh * S + q];
-        }
-        __syncthreads();
+        const int buf = (qb - qb_begin) & 1, q0 = qb * KVSTEP;
+        if (qb + 1 < qb_end) gload(q0 + KVSTEP);
+        const uint8_t* q_t = qo_t[buf][0];
+        const uint8_t* do_t = qo_t[buf][1];
+        const float* lse_t = ld_t[buf][0];
+        const float* dv_t = ld_t[buf][1];
 
-        // S = Q K^T and dP = dO V^T for the 64 queries x this wave's 32 keys
-        bf16x8_t pa[2][2], sa[2][2];  // P and dS as A operands: [32-query half][16-query step]
+        // S = Q K^T and dP = dO V^T for the 32 queries x this wave's 32 keys
+        bf16x8_t pa[1][2], sa[1][2];  // P and dS as A operands: [16-query step]
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 1; ++h) {
             f32x16_t s = zero16(), dp = zero16();
+            // (compiler-scheduled reads: a read pipeline here needs registers
+            // this kernel does not have at two waves per SIMD)
 #pragma unroll
             for (int ks = 0; ks < C::KS; ++ks) {
-                const bf16x8_t kf = row_frag<D>(k_t, krow, ks, g);
-                const bf16x8_t vf = row_frag<D>(v_t, krow, ks, g);
-                s = mfma(row_frag<D>(q_t, h * 32 + col, ks, g), kf, s);
-                dp = mfma(row_frag<D>(do_t, h * 32 + col, ks, g), vf, dp);
+                s = mfma(row_frag<D>(q_t, h * 32 + col, ks, g), kf[ks], s);
+                dp = mfma(row_frag<D>(do_t, h * 32 + col, ks, g), row_frag<D>(v_t, vrow, ks, g), dp);
             }
-            // register r: query h*32 + 8(r/4) + 4g + r%4 of this step
+            // register r: query 8(r/4) + 4g + r%4 of this block
             float p[16], ds[16];
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
@@ -214,7 +349,7 @@ __global__ __launch_bounds__(BT, 1) void flash_bwd_dkdv_kernel(
                 for (int i = 0; i < 4; ++i) {
                     const int r = 4 * r4 + i, q = q0 + ql + i;
                     const bool live = q < S && (!CAUSAL || key <= q);
-                    const float pv = live ? exp2f(s[r] * c - l4[i]) : 0.0f;
+                    const float pv = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -l4[i])) : 0.0f;
                     p[r] = pv;
                     ds[r] = pv * (dp[r] - d4[i]);
                 }
@@ -227,16 +362,25 @@ __global__ __launch_bounds__(BT, 1) void flash_bwd_dkdv_kernel(
         }
         // dV += P^T dO, dK += dS^T Q: A = P / dS (this lane's key), B read
         // transposed in the matching query order
+        // MFMA m = (dt, t, which): which 0 = dV (dO read), 1 = dK (Q read);
+        // the reads of MFMAs m+1 and m+2 are in flight while m runs
+        tr_pipeline<D, 4 * C::DT, 2>(
+            [&](int m) { return tr_addr<D>((m & 1) ? q_t : do_t, 16 * ((m >> 1) & 1), m >> 2, lane); },
+            [&](auto mi, bf16x8_t b) {
+                constexpr int m = decltype(mi)::value, dt = m >> 2, t = (m >> 1) & 1;
+                if constexpr (m & 1) dk[dt] = mfma(sa[0][t], b, dk[dt]);
+                else dv[dt] = mfma(pa[0][t], b, dv[dt]);
+            });
+        // keep the transposing reads two MFMAs ahead of their use
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int rb = h * 32 + 16 * t;
-                    dv[dt] = mfma(pa[h][t], tr_frag<D>(do_t, rb, dt, lane), dv[dt]);
-                    dk[dt] = mfma(sa[h][t], tr_frag<D>(q_t, rb, dt, lane), dk[dt]);
-                }
+        for (int i = 0; i < 4 * C::DT - 2; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        if (qb + 1 < qb_end) sstore(buf ^ 1);
+        __syncthreads();
     }
 
     // dK = scale * dS^T Q, dV = P^T dO; register r of block dt: key row
@@ -245,30 +389,41 @@ __global__ __launch_bounds__(BT, 1) void flash_bwd_dkdv_kernel(
     for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int kr = k0 + wave * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (kr >= S) continue;
-            const int64_t o = hoff + (int64_t)kr * D + 32 * dt + col;
+            const int kk = k0 + wave * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (kk >= S) continue;
+            const int64_t o = hoff + (int64_t)kk * D + 32 * dt + col;
             dK[o] = __builtin_bit_cast(uint16_t, (__bf16)(dk[dt][r] * scale));
             dV[o] = __builtin_bit_cast(uint16_t, (__bf16)dv[dt][r]);
         }
 }
 
 // ---- 3. dQ ----------------------------------------------------------------------
+// 8 waves x 32 queries (two waves per SIMD).  K/V tiles of 64 keys are double
+// buffered in LDS: the global loads of tile t+1 are issued into registers
+// before tile t is multiplied and stored to the other buffer after, one
+// barrier per tile.
+constexpr int QW = 8;             // waves per dQ workgroup
+constexpr int QT = QW * 64;
+constexpr int QOWN = QW * 32;     // queries per dQ workgroup
+
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(BT, 1) void flash_bwd_dq_kernel(
+__global__ __launch_bounds__(QT, 1) void flash_bwd_dq_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dvec,
     uint16_t* __restrict__ dQ, int S, float scale) {
     using C = BwdCfg<D>;
-    __shared__ __attribute__((aligned(16))) uint8_t k_t[BSTEP * C::PITCH];
-    __shared__ __attribute__((aligned(16))) uint8_t v_t[BSTEP * C::PITCH];
+    constexpr int UNITS = D / 8;                      // 16-byte units per row
+    constexpr int PF = 2 * BSTEP * UNITS / QT;        // prefetched units per thread (K then V)
+    __shared__ __attribute__((aligned(16))) uint8_t kv_t[2][2][BSTEP * C::PITCH];  // [buf][K, V]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
-    const int nqb = (S + BOWN - 1) / BOWN;
+    const int nqb = (S + QOWN - 1) / QOWN;
     const int bh = blockIdx.x / nqb;
-    const int q0 = (nqb - 1 - blockIdx.x % nqb) * BOWN;  // longest causal range first
+    const int q0 = (nqb - 1 - blockIdx.x % nqb) * QOWN;  // longest causal range first
     const int64_t hoff = (int64_t)bh * S * D;
+    const uint16_t* Kh = K + hoff;
+    const uint16_t* Vh = V + hoff;
     const float c = scale * kLog2e;
 
     // this lane's query (S^T / dP^T column) and its Q, dO fragments (B operands)
@@ -283,46 +438,76 @@ __global__ __launch_bounds__(BT, 1) void flash_bwd_dq_kernel(
     const float lse2 = lse[(int64_t)bh * S + qr] * kLog2e;
     const float dvq = dvec[(int64_t)bh * S + qr];
 
+    // tile loads: unit e = tid + QT p of the 2 x 64 rows (K rows, then V rows)
+    u32x4_t pf[PF];
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int e = tid + QT * p;
+            const int r = (e / UNITS) % BSTEP, u = e % UNITS;
+            const int64_t gr = min(kb + r, S - 1);
+            const uint16_t* src = (e / UNITS < BSTEP ? Kh : Vh) + gr * D + 8 * u;
+            pf[p] = *reinterpret_cast<const u32x4_t*>(src);
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int e = tid + QT * p;
+            const int r = (e / UNITS) % BSTEP, u = e % UNITS;
+            *reinterpret_cast<u32x4_t*>(&kv_t[buf][e / UNITS / BSTEP][r * C::PITCH + 16 * u]) = pf[p];
+        }
+    };
+
     f32x16_t dq[C::DT];
 #pragma unroll
     for (int i = 0; i < C::DT; ++i) dq[i] = zero16();
 
-    const int kv_end = CAUSAL ? min(S, q0 + BOWN) : S;
-    for (int kb = 0; kb < kv_end; kb += BSTEP) {
-        __syncthreads();
-        load_tile<D>(k_t, K + hoff, kb, BSTEP, S, tid);
-        load_tile<D>(v_t, V + hoff, kb, BSTEP, S, tid);
-        __syncthreads();
+    const int kv_end = CAUSAL ? min(S, q0 + QOWN) : S;
+    const int nt = (kv_end + BSTEP - 1) / BSTEP;  // >= 1
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int t = 0; t < nt; ++t) {
+        const int buf = t & 1, kb = t * BSTEP;
+        if (t + 1 < nt) gload(kb + BSTEP);
+        const uint8_t* k_t = kv_t[buf][0];
+        const uint8_t* v_t = kv_t[buf][1];
         // S^T = K Q^T, dP^T = V dO^T: 64 keys x this wave's 32 queries
         bf16x8_t sb[2][2];  // dS^T as B operands: [32-key half][16-key step]
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             f32x16_t s = zero16(), dp = zero16();
-#pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
-                s = mfma(row_frag<D>(k_t, h * 32 + col, ks, g), qf[ks], s);
-                dp = mfma(row_frag<D>(v_t, h * 32 + col, ks, g), of[ks], dp);
-            }
+            // S^T and dP^T MFMAs alternate: m = 2 ks + which
+            row_pipeline<2 * C::KS, 1, 2>(
+                [&](int m, int) { return row_addr<D>((m & 1) ? v_t : k_t, h * 32 + col, m >> 1, g); },
+                [&](auto mi, u32x4_t* f) {
+                    constexpr int m = decltype(mi)::value;
+                    if constexpr (m & 1) dp = mfma(as_bf16x8(f[0]), of[m >> 1], dp);
+                    else s = mfma(as_bf16x8(f[0]), qf[m >> 1], s);
+                });
             // register r: key kb + h*32 + 8(r/4) + 4g + r%4
             float ds[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int k = kb + h * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
                 const bool live = k < S && q < S && (!CAUSAL || k <= q);
-                const float pv = live ? exp2f(s[r] * c - lse2) : 0.0f;
+                const float pv = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -lse2)) : 0.0f;
                 ds[r] = pv * (dp[r] - dvq);
             }
 #pragma unroll
-            for (int t = 0; t < 2; ++t) sb[h][t] = pack8(ds + 8 * t);
+            for (int t2 = 0; t2 < 2; ++t2) sb[h][t2] = pack8(ds + 8 * t2);
         }
         // dQ^T += K^T dS^T: A = K read transposed in the matching key order
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
-                    dq[dt] = mfma(tr_frag<D>(k_t, h * 32 + 16 * t, dt, lane), sb[h][t], dq[dt]);
+        // MFMA m = (dt, h, t2); the reads of MFMAs m+1 and m+2 are in flight
+        tr_pipeline<D, 4 * C::DT, 2>(
+            [&](int m) { return tr_addr<D>(k_t, 16 * (m & 3), m >> 2, lane); },
+            [&](auto mi, bf16x8_t a) {
+                constexpr int m = decltype(mi)::value, dt = m >> 2, h = (m >> 1) & 1, t2 = m & 1;
+                dq[dt] = mfma(a, sb[h][t2], dq[dt]);
+            });
+        if (t + 1 < nt) sstore(buf ^ 1);
+        __syncthreads();
     }
 
     // dQ = scale * dS K; register r of block dt: head dim 32 dt + 8(r/4) +
@@ -351,7 +536,8 @@ hipError_t launch_bwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, c
     const int nb = (S + BOWN - 1) / BOWN;
     hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, CAUSAL>), dim3(BH * nb), dim3(BT), 0, s, Q, K, V, dO,
                        lse, dvec, dK, dV, S, scale);
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, CAUSAL>), dim3(BH * nb), dim3(BT), 0, s, Q, K, V, dO,
+    const int nqb = (S + QOWN - 1) / QOWN;
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, CAUSAL>), dim3(BH * nqb), dim3(QT), 0, s, Q, K, V, dO,
                        lse, dvec, dQ, S, scale);
     return hipGetLastError();
 }
