@@ -242,6 +242,22 @@ int jules_hip_cross_entropy(const float* logits, const int32_t* targets,
                             void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* ---- 2-layer MLP forward ---------------------------------------------------
+ * output [M,N2] = relu(X W1 + b1) W2 + b2, fp32 row-major; X [M,K1],
+ * W1 [K1,N1], b1 [N1], W2 [N1,N2], b2 [N2].
+ * Replaces fusedMLPForward(output, X, MLPParams{W1,b1,W2,b2,M,K1,N1,N2},
+ * arena, planner) (FusedKernels.h:650-760); routed name "fusedMLPForward"
+ * (KernelRoutingPass.h:20): (X, W1, b1, W2, b2) -> output.  The products are
+ * fp32 MFMA GEMMs (the reference's are BLAS calls: results agree to fp32
+ * rounding).  workspace: jules_hip_mlp_forward_workspace_size(M,K1,N1,N2)
+ * bytes (the hidden activations), 16-byte aligned, no initialisation.
+ */
+size_t jules_hip_mlp_forward_workspace_size(int M, int K1, int N1, int N2);
+int jules_hip_mlp_forward(const float* X, const float* W1, const float* b1,
+                          const float* W2, const float* b2, float* output,
+                          int M, int K1, int N1, int N2,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- 2-layer MLP forward + loss + backward --------------------------------
  * Replaces interleavedMLPForwardBackward (include/jules/Kernel/
  * InterleavedAutodiff.h:55-62): same operands in the same order, minus the

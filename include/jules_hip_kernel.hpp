@@ -111,6 +111,19 @@ void fusedLayerNorm(float* output, const float* input, const float* gamma, const
                     int M, int N, float epsilon = 1e-5f);
 // reference FusedKernels.h:766; returns the mean loss (NaN on failure)
 float fusedCrossEntropyLoss(const float* logits, const int32_t* targets, float* grad, int M, int N);
+// reference FusedKernels.h:650-657, :659
+struct MLPParams {
+    const float* W1;
+    const float* b1;
+    const float* W2;
+    const float* b2;
+    int batch_size;
+    int in_features;
+    int hidden_features;
+    int out_features;
+};
+void fusedMLPForward(float* output, const float* X, const MLPParams& params, ExecutionArena& arena,
+                     TilePlanner& planner);
 // reference InterleavedAutodiff.h:41-53
 struct MLPGradients {
     float* dW1;

@@ -53,6 +53,8 @@ SIGNATURES = {
     "jules_hip_layernorm": (_int, [_vp, _vp, _vp, _vp, _int, _int, _f32, _vp]),
     "jules_hip_cross_entropy_workspace_size": (_size, [_int]),
     "jules_hip_cross_entropy": (_int, [_vp, _vp, _vp, _vp, _int, _int, _vp, _size, _vp]),
+    "jules_hip_mlp_forward_workspace_size": (_size, [_int, _int, _int, _int]),
+    "jules_hip_mlp_forward": (_int, [_vp] * 6 + [_int] * 4 + [_vp, _size, _vp]),
     "jules_hip_mlp_workspace_size": (_size, [_int, _int, _int, _int]),
     "jules_hip_mlp_forward_backward": (_int, [_vp] * 12 + [_int, _int, _int, _int, _vp, _vp, _size,
                                                            _vp]),

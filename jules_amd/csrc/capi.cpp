@@ -296,6 +296,34 @@ int jules_hip_cross_entropy(const float* logits, const int32_t* targets, float* 
                      "cross_entropy launch");
 }
 
+size_t jules_hip_mlp_forward_workspace_size(int M, int K1, int N1, int N2) {
+    if (M < 0 || K1 < 1 || N1 < 1 || N2 < 1) return 0;
+    return jh::mlp_forward_workspace_size(M, K1, N1, N2);
+}
+
+int jules_hip_mlp_forward(const float* X, const float* W1, const float* b1, const float* W2,
+                          const float* b2, float* output, int M, int K1, int N1, int N2,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    if (M < 0 || K1 < 1 || N1 < 1 || N2 < 1)
+        return fail(JH_ERR_SHAPE, "mlp forward: needs M >= 0 and K1, N1, N2 >= 1 (got %d %d %d %d)",
+                    M, K1, N1, N2);
+    if ((int64_t)M * K1 > kMaxElems || (int64_t)M * N1 > kMaxElems || (int64_t)M * N2 > kMaxElems ||
+        (int64_t)K1 * N1 > kMaxElems || (int64_t)N1 * N2 > kMaxElems)
+        return fail(JH_ERR_SHAPE, "mlp forward: too large");
+    if (M == 0) return JH_OK;
+    if (!X || !W1 || !b1 || !W2 || !b2 || !output) return fail(JH_ERR_NULL, "mlp forward: null operand");
+    const void* ptrs[] = {X, W1, b1, W2, b2, output};
+    for (const void* q : ptrs)
+        if (!aligned(q, 4)) return fail(JH_ERR_ALIGN, "mlp forward: operands must be 4-byte aligned");
+    const size_t need = jh::mlp_forward_workspace_size(M, K1, N1, N2);
+    if (!workspace || workspace_bytes < need)
+        return fail(JH_ERR_WORKSPACE, "mlp forward: workspace %zu bytes, need %zu", workspace_bytes, need);
+    if (!aligned(workspace, 16)) return fail(JH_ERR_ALIGN, "mlp forward: workspace alignment");
+    return check_hip(jh::launch_mlp_forward(X, W1, b1, W2, b2, output, M, K1, N1, N2, workspace,
+                                            static_cast<hipStream_t>(stream)),
+                     "mlp forward launch");
+}
+
 size_t jules_hip_mlp_workspace_size(int M, int K1, int N1, int N2) {
     if (M < 0 || K1 < 1 || N1 < 1 || N2 < 1) return 0;
     return jh::mlp_workspace_size(M, K1, N1, N2);
@@ -630,6 +658,35 @@ int k_cross_entropy(int ni, const jh_tensor* in, int no, jh_tensor* out, const c
                                    static_cast<float*>(addr_mut(l)), (int)M, (int)N, ws, need, s);
 }
 
+int k_mlp_forward(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
+    if (ni != 5 || no != 1 || !in || !out)
+        return fail(JH_ERR_ARG, "fusedMLPForward: (X, W1, b1, W2, b2) -> output");
+    const jh_tensor &x = in[0], &w1 = in[1], &b1 = in[2], &w2 = in[3], &b2 = in[4];
+    jh_tensor& y = out[0];
+    for (int i = 0; i < ni; ++i)
+        if (!contiguous(in[i]) || in[i].dtype != JH_F32)
+            return fail(JH_ERR_DTYPE, "fusedMLPForward: contiguous fp32 operands");
+    if (!contiguous(y) || y.dtype != JH_F32) return fail(JH_ERR_DTYPE, "fusedMLPForward: fp32 output");
+    if (x.rank != 2 || w1.rank != 2 || w2.rank != 2)
+        return fail(JH_ERR_SHAPE, "fusedMLPForward: X, W1, W2 rank 2");
+    const int64_t M = x.sizes[0], K1 = x.sizes[1], N1 = w1.sizes[1], N2 = w2.sizes[1];
+    if (w1.sizes[0] != K1 || w2.sizes[0] != N1 || numel(b1) != N1 || numel(b2) != N2 ||
+        numel(y) != M * N2)
+        return fail(JH_ERR_SHAPE, "fusedMLPForward: operand shapes disagree");
+    if (M > INT32_MAX || K1 > INT32_MAX || N1 > INT32_MAX || N2 > INT32_MAX)
+        return fail(JH_ERR_SHAPE, "fusedMLPForward: too large");
+    const size_t need = jules_hip_mlp_forward_workspace_size((int)M, (int)K1, (int)N1, (int)N2);
+    void* ws = nullptr;
+    if (need > 0) {
+        const int st = registry_workspace(need, &ws);
+        if (st != JH_OK) return st;
+    }
+    return jules_hip_mlp_forward(static_cast<const float*>(addr(x)), static_cast<const float*>(addr(w1)),
+                                 static_cast<const float*>(addr(b1)), static_cast<const float*>(addr(w2)),
+                                 static_cast<const float*>(addr(b2)), static_cast<float*>(addr_mut(y)),
+                                 (int)M, (int)K1, (int)N1, (int)N2, ws, need, s);
+}
+
 int k_mlp(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
     if (ni != 6 || (no != 6 && no != 7) || !in || !out)
         return fail(JH_ERR_ARG, "interleavedMLPForwardBackward: (X, W1, b1, W2, b2, targets) -> "
@@ -690,6 +747,7 @@ const Entry kRegistry[] = {
     {"fusedSoftmax", k_softmax},
     {"fusedLayerNorm", k_layernorm},
     {"fusedCrossEntropyLoss", k_cross_entropy},
+    {"fusedMLPForward", k_mlp_forward},
     {"interleavedMLPForwardBackward", k_mlp},
     {"fusedMatmul", k_matmul},
     {"fusedMatmulBias", k_matmul_bias},

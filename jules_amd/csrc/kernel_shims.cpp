@@ -224,6 +224,31 @@ void fusedLayerNorm(float* output, const float* input, const float* gamma, const
     record(st);
 }
 
+void fusedMLPForward(float* output, const float* X, const MLPParams& p, ExecutionArena&,
+                     TilePlanner&) {
+    const int M = p.batch_size, K1 = p.in_features, N1 = p.hidden_features, N2 = p.out_features;
+    if (M < 0 || K1 < 1 || N1 < 1 || N2 < 1) {
+        record(JH_ERR_SHAPE);
+        return;
+    }
+    const size_t f = sizeof(float), m = (size_t)M, k1 = (size_t)K1, n1 = (size_t)N1, n2 = (size_t)N2;
+    std::vector<char> ws_host(std::max<size_t>(16, jules_hip_mlp_forward_workspace_size(M, K1, N1, N2)));
+    DevBuf x(X, f * m * k1, true, false), w1(p.W1, f * k1 * n1, true, false),
+        b1(p.b1, f * n1, true, false), w2(p.W2, f * n1 * n2, true, false), b2(p.b2, f * n2, true, false),
+        o(output, f * m * n2, false, true), ws(ws_host.data(), ws_host.size(), false, false);
+    if (!x.ok() || !w1.ok() || !b1.ok() || !w2.ok() || !b2.ok() || !o.ok() || !ws.ok()) {
+        record(JH_ERR_HIP);
+        return;
+    }
+    int st = jules_hip_mlp_forward(static_cast<const float*>(x.get()), static_cast<const float*>(w1.get()),
+                                   static_cast<const float*>(b1.get()), static_cast<const float*>(w2.get()),
+                                   static_cast<const float*>(b2.get()), static_cast<float*>(o.get()), M,
+                                   K1, N1, N2, ws.get(), ws_host.size(), nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !o.finish()) st = JH_ERR_HIP;
+    record(st);
+}
+
 InterleavedMLPResult interleavedMLPForwardBackward(const float* X, const float* W1,
                                                    const float* b1, const float* W2,
                                                    const float* b2, const int32_t* targets,

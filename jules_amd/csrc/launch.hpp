@@ -39,6 +39,10 @@ hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, flo
                                 float* loss, float* row_loss, int M, int N, hipStream_t s);
 
 // 2-layer MLP forward + softmax cross entropy + backward (mlp.hip)
+size_t mlp_forward_workspace_size(int M, int K1, int N1, int N2);
+hipError_t launch_mlp_forward(const float* X, const float* W1, const float* b1, const float* W2,
+                              const float* b2, float* output, int M, int K1, int N1, int N2,
+                              void* ws, hipStream_t s);
 size_t mlp_workspace_size(int M, int K1, int N1, int N2);
 hipError_t launch_mlp_forward_backward(const float* X, const float* W1, const float* b1,
                                        const float* W2, const float* b2, const int32_t* targets,

@@ -324,6 +324,28 @@ size_t mlp_workspace_size(int M, int K1, int N1, int N2) {
            align256((size_t)S * (N1 > N2 ? N1 : N2) * sizeof(float)) + align256(kp * sizeof(float));
 }
 
+// fusedMLPForward (reference FusedKernels.h:659-760): output = relu(X W1 +
+// b1) W2 + b2, the forward half of the step below.  workspace: the hidden
+// activations [M,N1], then split-K partials
+size_t mlp_forward_workspace_size(int M, int K1, int N1, int N2) {
+    (void)K1;
+    const size_t kp = std::max(kplan_floats(M, N1, K1), kplan_floats(M, N2, N1));
+    return align256((size_t)M * N1 * sizeof(float)) + align256(kp * sizeof(float));
+}
+
+hipError_t launch_mlp_forward(const float* X, const float* W1, const float* b1, const float* W2,
+                              const float* b2, float* output, int M, int K1, int N1, int N2,
+                              void* ws, hipStream_t s) {
+    if (M == 0) return hipSuccess;
+    float* act = static_cast<float*>(ws);
+    float* kpart = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                            align256((size_t)M * N1 * sizeof(float)));
+    hipError_t e;
+    if ((e = gemm<false, false, EPI_BIAS_RELU>(X, K1, W1, N1, act, N1, M, N1, K1, b1, nullptr, 0, kpart, s)))
+        return e;
+    return gemm<false, false, EPI_BIAS>(act, N1, W2, N2, output, N2, M, N2, N1, b2, nullptr, 0, kpart, s);
+}
+
 hipError_t launch_mlp_forward_backward(const float* X, const float* W1, const float* b1,
                                        const float* W2, const float* b2, const int32_t* targets,
                                        float* output, float* dW1, float* db1, float* dW2, float* db2,

@@ -224,6 +224,29 @@ def cross_entropy(logits, targets, grad=None, loss=None, workspace=None):
     return loss, grad
 
 
+def mlp_forward(X, W1, b1, W2, b2, out=None, workspace=None):
+    """fusedMLPForward (FusedKernels.h:659): relu(X W1 + b1) W2 + b2, fp32."""
+    _need(X, "X", (torch.float32,))
+    for t, n in ((W1, "W1"), (b1, "b1"), (W2, "W2"), (b2, "b2")):
+        _need(t, n, (torch.float32,), X.device)
+    M, K1 = X.shape
+    K1b, N1 = W1.shape
+    N1b, N2 = W2.shape
+    if K1b != K1 or N1b != N1 or b1.numel() != N1 or b2.numel() != N2:
+        raise ValueError("mlp forward: operand shapes disagree")
+    if out is None:
+        out = torch.empty((M, N2), dtype=torch.float32, device=X.device)
+    elif tuple(out.shape) != (M, N2):
+        raise ValueError("mlp forward: out must be [M, N2]")
+    _need(out, "out", (torch.float32,), X.device)
+    if workspace is None:
+        nbytes = lib().jules_hip_mlp_forward_workspace_size(M, K1, N1, N2)
+        workspace = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=X.device)
+    check(lib().jules_hip_mlp_forward(_ptr(X), _ptr(W1), _ptr(b1), _ptr(W2), _ptr(b2), _ptr(out),
+                                      M, K1, N1, N2, _ptr(workspace), workspace.numel(), _stream(X)))
+    return out
+
+
 def mlp_workspace(M, K1, N1, N2, device):
     nbytes = lib().jules_hip_mlp_workspace_size(int(M), int(K1), int(N1), int(N2))
     return torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)

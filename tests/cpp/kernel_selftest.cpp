@@ -1,7 +1,8 @@
 // kernel_selftest.cpp - exercises the jules::kernel C++ entry points of
 // include/jules_hip_kernel.hpp with host buffers (staged to and from the GPU
-// by the library) on GPU 0: interleavedMLPForwardBackward against a
-// double-precision loop restatement of the same formulas.  Prints
+// by the library) on GPU 0: interleavedMLPForwardBackward and
+// fusedMLPForward against a double-precision loop restatement of the same
+// formulas.  Prints
 // "kernel selftest ok" and exits 0 when every check holds.  Built by
 // jules_amd/build.py, run by tests/test_gpu_mlp.py.
 #include <cmath>
@@ -110,6 +111,16 @@ int main() {
                                       out.data(), dW1.data(), db1.data(), dW2.data(), db2.data(),
                                       nullptr, M, K1, 0, N2, arena, planner);
     CHECK(lastStatus() == JH_ERR_SHAPE && std::isnan(r.loss));
+
+    // fusedMLPForward (FusedKernels.h:659): the same forward, no loss
+    std::vector<float> fwd(M * N2, -7.0f);
+    const MLPParams p{W1.data(), b1.data(), W2.data(), b2.data(), M, K1, N1, N2};
+    fusedMLPForward(fwd.data(), X.data(), p, arena, planner);
+    CHECK(lastStatus() == JH_OK);
+    CHECK(max_rel(fwd, o) < 1e-5);
+    const MLPParams bad{W1.data(), b1.data(), W2.data(), b2.data(), M, 0, N1, N2};
+    fusedMLPForward(fwd.data(), X.data(), bad, arena, planner);
+    CHECK(lastStatus() == JH_ERR_SHAPE);
     std::printf("kernel selftest ok\n");
     return 0;
 }

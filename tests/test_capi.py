@@ -44,7 +44,7 @@ def test_cxx_shim_symbols_exported():
     names = ["fusedMatmulRelu", "fusedMatmulBiasRelu", "tiledMatmulWithActivation", "fusedGelu",
              "matmulInt8", "flashAttention", "attention", "standardAttention", "lastStatus",
              "fusedSoftmax", "fusedLayerNorm", "fusedCrossEntropyLoss",
-             "interleavedMLPForwardBackward"]
+             "fusedMLPForward", "interleavedMLPForwardBackward"]
     for n in names:
         assert re.search(rf"\b{n}\s*\(", text), n
         mangled = f"_ZN5jules6kernel{len(n)}{n}E"
@@ -65,7 +65,7 @@ def test_registry_names():
     routed = ["fusedMatmulRelu", "fusedMatmulSigmoid", "fusedMatmulTanh", "fusedMatmulGelu",
               "fusedMatmulBiasRelu", "fusedMatmulBiasSigmoid", "fusedMatmulBiasTanh",
               "fusedGelu", "matmulInt8", "flashAttention", "fusedSoftmax", "fusedLayerNorm",
-              "fusedCrossEntropyLoss", "interleavedMLPForwardBackward"]
+              "fusedCrossEntropyLoss", "fusedMLPForward", "interleavedMLPForwardBackward"]
     added = ["fusedMatmulBiasGelu", "flashAttentionCausal", "matmulW8A16BiasSilu"]
     for n in routed + added:
         assert n in names
@@ -217,3 +217,19 @@ def test_mlp_validation():
     bad = list(args)
     bad[17] = 0  # workspace bytes
     assert f(*bad) == WS
+
+
+def test_mlp_forward_validation():
+    L = _lib.lib()
+    f = L.jules_hip_mlp_forward
+    assert L.jules_hip_mlp_forward_workspace_size(4, 3, 0, 2) == 0
+    assert L.jules_hip_mlp_forward_workspace_size(4, 3, 5, 2) >= 4 * 5 * 4
+    args = [P] * 6 + [4, 3, 5, 2, P, 1 << 20, None]
+    for i, code in ((7, SHAPE), (2, NULL), (11, WS)):
+        bad = list(args)
+        bad[i] = 0 if i != 2 else None
+        assert f(*bad) == code, i
+    bad = list(args)
+    bad[0] = P + 2  # X misaligned
+    assert f(*bad) == ALIGN
+    assert f(*([P] * 6 + [0, 3, 5, 2, None, 0, None])) == 0  # M = 0: nothing to do

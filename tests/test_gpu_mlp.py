@@ -121,9 +121,43 @@ def test_registry_path(dev):
     _check(got, ins)
 
 
+@pytest.mark.parametrize("M,K1,N1,N2", [(64, 784, 256, 10), (1, 1, 1, 1), (37, 50, 33, 10),
+                                        (257, 64, 300, 1000), (2048, 512, 384, 100), (8, 4096, 4096, 8)])
+def test_forward_against_fp64(dev, M, K1, N1, N2):
+    """fusedMLPForward (FusedKernels.h:659-760): relu(X W1 + b1) W2 + b2,
+    within 1e-5 of the oracle's forward; two calls in a row agree bit for
+    bit, and the forward agrees with the forward half of the training step
+    bit for bit (same GEMMs, same split plan)."""
+    case(f"mlp forward {M}x{K1}x{N1}x{N2}")
+    ins = I.mlp_inputs(M, K1, N1, N2, seed=M * 3 + K1 + N1 + N2, scaled=True)
+    X, W1, b1, W2, b2 = (to_dev(a, torch.float32, dev) for a in ins[:5])
+    y = ops.mlp_forward(X, W1, b1, W2, b2)
+    ref = po.mlp_forward_backward64(*ins)["output"]
+    err = I.rel_err(to_np(y), ref)
+    assert err < TOL, f"rel err {err:.3g}"
+    assert torch.equal(y, ops.mlp_forward(X, W1, b1, W2, b2))
+    if N2 > 1:
+        step = ops.mlp_forward_backward(X, W1, b1, W2, b2, to_dev(ins[5], torch.int32, dev))
+        assert torch.equal(y, step["output"])
+
+
+def test_forward_zero_rows_and_registry(dev):
+    case("mlp forward M=0 and registry fusedMLPForward")
+    X, W1, b1, W2, b2, _ = ins = I.mlp_inputs(21, 40, 24, 7, seed=5, scaled=True)
+    d = [to_dev(a, torch.float32, dev) for a in (X, W1, b1, W2, b2)]
+    assert ops.mlp_forward(d[0][:0], *d[1:]).shape == (0, 7)
+    out = torch.full((21, 7), float("nan"), dtype=torch.float32, device=dev)
+    st = registry_call("fusedMLPForward", d, [out])
+    assert st == 0, _lib.lib().jules_hip_last_error()
+    assert I.rel_err(to_np(out), po.mlp_forward_backward64(*ins)["output"]) < TOL
+    st = registry_call("fusedMLPForward", d[:4], [out])
+    assert st != 0
+
+
 def test_cxx_kernel_selftest(dev):
-    """jules::kernel::interleavedMLPForwardBackward with host buffers, from a
-    C++ program, against its own double-precision loops."""
+    """jules::kernel::interleavedMLPForwardBackward and fusedMLPForward with
+    host buffers, from a C++ program, against its own double-precision
+    loops."""
     case("kernel C++ selftest")
     exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "cpp",
                        "kernel_selftest")
