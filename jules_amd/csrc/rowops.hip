@@ -13,16 +13,16 @@
 // The sums are taken in a different (fixed, tree) order than the reference's
 // 16 lane partials, so results match it to rounding, not bit for bit.
 //
-// All three are HBM-bound.  One wave owns a row; with N <= 4096 the row is
-// held in registers (ELEMS elements per lane, element j = lane + 64 * t, so
-// every load and store instruction covers 256 contiguous bytes), read from
-// HBM once and written once, four rows per workgroup.  Longer rows get a
-// 256-thread workgroup each and three passes over the row (max, sum, write:
-// the reference's own pass structure, with the exponentials recomputed in the
-// last pass instead of stored); the loads of a pass are unrolled four deep
-// and the re-reads of a row mostly hit the MALL.  Reductions are a fixed
-// butterfly within a wave and a fixed order across waves, so results are
-// deterministic.
+// All three are HBM-bound, and the row is held in registers so it is read
+// from HBM once and written once: one wave per row for N <= 4096 (four rows
+// per workgroup), one 1024-thread workgroup per row for N <= 32768.  With
+// N % 4 == 0 and 16-byte aligned rows each thread moves 16-byte pieces,
+// otherwise single floats; either way every wave instruction covers
+// contiguous bytes.  Rows longer than 32768 get a 256-thread workgroup and
+// three passes over the row (max, sum, write: the reference's own pass
+// structure, the exponentials recomputed in the last pass).  Reductions are a
+// fixed butterfly within a wave and a fixed tree across waves, so results
+// are deterministic.
 #include <cfloat>
 
 #include "common.hpp"
@@ -32,7 +32,9 @@ namespace jh {
 namespace {
 
 constexpr int ROWS_PER_BLOCK = 4;
-constexpr int MAX_CACHED = 4096;  // longest row held in registers
+constexpr int MAX_CACHED = 4096;      // longest row held in one wave's registers
+constexpr int BT = 1024;              // threads of a block that holds one row
+constexpr int MAX_BLOCK_CACHED = 32768;  // longest row held in a block's registers
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -56,69 +58,170 @@ __device__ __forceinline__ float row_norm(float e, float inv, float sum, int j, 
     return j < nv ? e * inv : e / sum;
 }
 
-// ---- softmax over one row held in registers ----
-template <int ELEMS>
-__device__ __forceinline__ float softmax_cached(float (&v)[ELEMS], const float* x, int N,
-                                                int lane) {
+// ---- a row held in the registers of a group of G threads (one wave, or
+// the BT threads of a block).  Thread `tid` holds ELEMS elements: with VEC,
+// 16-byte pieces f = tid + G*t, elements 4f .. 4f+3 (rows 16-byte aligned,
+// N % 4 == 0); without, elements j = tid + G*t.  Every load or store
+// instruction of a wave covers contiguous bytes. ----
+template <int G, int ELEMS, bool VEC>
+struct RowRegs {
+    static constexpr int W = VEC ? 4 : 1;   // elements per access
+    static constexpr int NA = ELEMS / W;    // accesses per thread
+    float v[ELEMS];
+    __device__ __forceinline__ static int elem(int tid, int a, int i) {
+        return VEC ? 4 * (tid + G * a) + i : tid + G * a;
+    }
+    // v[] = x[] (pad outside the row)
+    __device__ __forceinline__ void load(const float* __restrict__ x, int N, int tid, float pad) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const int j0 = elem(tid, a, 0);
+            if constexpr (VEC) {
+                f32x4_t q = {pad, pad, pad, pad};
+                if (j0 < N) q = *reinterpret_cast<const f32x4_t*>(x + j0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[4 * a + i] = q[i];
+            } else {
+                v[a] = j0 < N ? x[j0] : pad;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float* __restrict__ y, int N, int tid) const {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const int j0 = elem(tid, a, 0);
+            if (j0 < N) {
+                if constexpr (VEC) {
+                    const f32x4_t q = {v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
+                    *reinterpret_cast<f32x4_t*>(y + j0) = q;
+                } else {
+                    y[j0] = v[a];
+                }
+            }
+        }
+    }
+    // f(element index, value) over this thread's elements inside the row
+    template <typename F>
+    __device__ __forceinline__ void each(int N, int tid, F&& f) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+                const int j = elem(tid, a, i);
+                f(j, v[W * a + i], j < N);
+            }
+    }
+};
+
+// group-wide reductions in a fixed order: a butterfly within each wave, then
+// (G = BT) the wave partials combined as a balanced tree through LDS
+template <int G>
+__device__ __forceinline__ float group_max(float v, float* red) {
+    v = wave_max(v);
+    if constexpr (G == 64) {
+        return v;
+    } else {
+        constexpr int NWV = G / 64;
+        __syncthreads();  // red is reused by consecutive reductions
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        float r[NWV];
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) r[w] = red[w];
+#pragma unroll
+        for (int h = NWV / 2; h > 0; h >>= 1)
+#pragma unroll
+            for (int w = 0; w < h; ++w) r[w] = fmaxf(r[w], r[w + h]);
+        return r[0];
+    }
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v, float* red) {
+    v = wave_sum(v);
+    if constexpr (G == 64) {
+        return v;
+    } else {
+        constexpr int NWV = G / 64;
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        float r[NWV];
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) r[w] = red[w];
+#pragma unroll
+        for (int h = NWV / 2; h > 0; h >>= 1)
+#pragma unroll
+            for (int w = 0; w < h; ++w) r[w] = r[w] + r[w + h];
+        return r[0];
+    }
+}
+
+// softmax of a held row (reference passes: max, exp and sum, scale); returns
+// the sum and leaves p in R.v
+template <bool FULL, int G, int ELEMS, bool VEC>
+__device__ __forceinline__ void softmax_held(RowRegs<G, ELEMS, VEC>& R, const float* x, int N,
+                                             int tid, float* red, float* mx_out, float* s_out) {
     const int nv = N & ~15;
+    R.load(x, N, tid, -FLT_MAX);
     float mx = -FLT_MAX;
 #pragma unroll
-    for (int t = 0; t < ELEMS; ++t) {
-        const int j = lane + 64 * t;
-        v[t] = j < N ? x[j] : -FLT_MAX;
-        mx = ref_max(mx, v[t]);
-    }
-    mx = wave_max(mx);
+    for (int k = 0; k < ELEMS; ++k) mx = ref_max(mx, R.v[k]);
+    mx = group_max<G>(mx, red);
     float s = 0.0f;
-#pragma unroll
-    for (int t = 0; t < ELEMS; ++t) {
-        const int j = lane + 64 * t;
-        const float e = j < N ? row_exp(v[t] - mx, j, nv) : 0.0f;
-        v[t] = e;
-        s += e;
+    // FULL: the row has no tail (N % 16 == 0, the common case), so every
+    // element takes fast_exp and the reciprocal product; a kernel of its own,
+    // which does not carry the registers of the libm tail path
+    if constexpr (FULL) {
+        R.each(N, tid, [&](int, float& e, bool in) {
+            e = in ? fast_exp(e - mx) : 0.0f;
+            s += e;
+        });
+    } else {
+        R.each(N, tid, [&](int j, float& e, bool in) {
+            e = in ? row_exp(e - mx, j, nv) : 0.0f;
+            s += e;
+        });
     }
-    s = wave_sum(s);
+    s = group_sum<G>(s, red);
     const float inv = 1.0f / s;
+    if constexpr (FULL) {
 #pragma unroll
-    for (int t = 0; t < ELEMS; ++t) v[t] = row_norm(v[t], inv, s, lane + 64 * t, nv);
-    return s;
+        for (int k = 0; k < ELEMS; ++k) R.v[k] *= inv;
+    } else {
+        R.each(N, tid, [&](int j, float& e, bool) { e = row_norm(e, inv, s, j, nv); });
+    }
+    *mx_out = mx;
+    *s_out = s;
 }
 
-template <int ELEMS>
-__global__ __launch_bounds__(256) void softmax_kernel(float* __restrict__ out,
-                                                      const float* __restrict__ in, int M, int N) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const float* x = in + (int64_t)row * N;
-    float* y = out + (int64_t)row * N;
-    float v[ELEMS];
-    softmax_cached<ELEMS>(v, x, N, lane);
-#pragma unroll
-    for (int t = 0; t < ELEMS; ++t) {
-        const int j = lane + 64 * t;
-        if (j < N) y[j] = v[t];
+// row of this block: one per wave (G = 64, ROWS_PER_BLOCK rows) or one per block
+template <int G>
+__device__ __forceinline__ int held_row(int* tid) {
+    if constexpr (G == 64) {
+        *tid = threadIdx.x & 63;
+        return blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+    } else {
+        *tid = threadIdx.x;
+        return blockIdx.x;
     }
 }
 
-// ---- rows longer than MAX_CACHED: one 256-thread workgroup per row ----
-constexpr int LT = 256;  // threads per long row
+template <int G, int ELEMS, bool VEC, bool FULL>
+__global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void softmax_kernel(
+    float* __restrict__ out, const float* __restrict__ in, int M, int N) {
+    __shared__ float red[G == 64 ? 1 : G / 64];
+    int tid;
+    const int row = held_row<G>(&tid);
+    if (row >= M) return;  // whole wave (G = 64) or whole block
+    RowRegs<G, ELEMS, VEC> R;
+    float mx, s;
+    softmax_held<FULL>(R, in + (int64_t)row * N, N, tid, red, &mx, &s);
+    R.store(out + (int64_t)row * N, N, tid);
+}
 
-// fixed-order reductions over the workgroup (4 waves)
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
-    __syncthreads();  // red is reused by consecutive reductions
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
+// ---- rows longer than a block holds: one 256-thread workgroup per row,
+// three passes ----
+constexpr int LT = 256;  // threads per long row
 
 // f(j) for j = tid, tid + 256, ... < N, four loads in flight
 template <typename F>
@@ -139,15 +242,15 @@ __device__ __forceinline__ void long_row_stats(const float* x, int N, float* red
     const int nv = N & ~15;
     float mx = -FLT_MAX;
     row_loop(N, [&](int j) { mx = ref_max(mx, x[j]); });
-    mx = block_max(mx, red);
+    mx = group_max<LT>(mx, red);
     float s = 0.0f;
     row_loop(N, [&](int j) { s += row_exp(x[j] - mx, j, nv); });
     *mx_out = mx;
-    *s_out = block_sum(s, red);
+    *s_out = group_sum<LT>(s, red);
 }
 
 __global__ __launch_bounds__(LT) void softmax_long_kernel(float* out, const float* in, int N) {
-    __shared__ float red[4];
+    __shared__ float red[LT / 64];
     const float* x = in + (int64_t)blockIdx.x * N;
     float* y = out + (int64_t)blockIdx.x * N;
     const int nv = N & ~15;
@@ -158,39 +261,43 @@ __global__ __launch_bounds__(LT) void softmax_long_kernel(float* out, const floa
 }
 
 // ---- layernorm ----
-template <int ELEMS>
-__global__ __launch_bounds__(256) void layernorm_kernel(float* __restrict__ out,
-                                                        const float* __restrict__ in,
-                                                        const float* __restrict__ gamma,
-                                                        const float* __restrict__ beta, int M,
-                                                        int N, float eps) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+template <int G, int ELEMS, bool VEC, bool FULL>
+__global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void layernorm_kernel(
+    float* __restrict__ out, const float* __restrict__ in, const float* __restrict__ gamma,
+    const float* __restrict__ beta, int M, int N, float eps) {
+    __shared__ float red[G == 64 ? 1 : G / 64];
+    int tid;
+    const int row = held_row<G>(&tid);
     if (row >= M) return;
-    const float* x = in + (int64_t)row * N;
-    float* y = out + (int64_t)row * N;
-    float v[ELEMS];
+    RowRegs<G, ELEMS, VEC> R;
+    R.load(in + (int64_t)row * N, N, tid, 0.0f);
     float s = 0.0f;
 #pragma unroll
-    for (int t = 0; t < ELEMS; ++t) {
-        const int j = lane + 64 * t;
-        v[t] = j < N ? x[j] : 0.0f;
-        s += v[t];
-    }
-    const float mean = wave_sum(s) / (float)N;
+    for (int k = 0; k < ELEMS; ++k) s += R.v[k];
+    const float mean = group_sum<G>(s, red) / (float)N;
     float q = 0.0f;
-#pragma unroll
-    for (int t = 0; t < ELEMS; ++t) {
-        const int j = lane + 64 * t;
-        const float d = v[t] - mean;
-        q = j < N ? __builtin_fmaf(d, d, q) : q;
-    }
-    const float var = wave_sum(q) / (float)N;
+    R.each(N, tid, [&](int, float& x, bool in) {
+        const float d = x - mean;
+        q = in ? __builtin_fmaf(d, d, q) : q;
+    });
+    const float var = group_sum<G>(q, red) / (float)N;
     const float inv_std = 1.0f / sqrtf(var + eps);
+    float* y = out + (int64_t)row * N;
+    using RR = RowRegs<G, ELEMS, VEC>;
 #pragma unroll
-    for (int t = 0; t < ELEMS; ++t) {
-        const int j = lane + 64 * t;
-        if (j < N) y[j] = __builtin_fmaf((v[t] - mean) * inv_std, gamma[j], beta[j]);
+    for (int a = 0; a < RR::NA; ++a) {
+        const int j0 = RR::elem(tid, a, 0);
+        if (j0 >= N) continue;
+        if constexpr (VEC) {
+            const f32x4_t gq = *reinterpret_cast<const f32x4_t*>(gamma + j0);
+            const f32x4_t bq = *reinterpret_cast<const f32x4_t*>(beta + j0);
+            f32x4_t o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf((R.v[4 * a + i] - mean) * inv_std, gq[i], bq[i]);
+            *reinterpret_cast<f32x4_t*>(y + j0) = o;
+        } else {
+            y[j0] = __builtin_fmaf((R.v[a] - mean) * inv_std, gamma[j0], beta[j0]);
+        }
     }
 }
 
@@ -198,81 +305,85 @@ __global__ __launch_bounds__(LT) void layernorm_long_kernel(float* out, const fl
                                                            const float* __restrict__ gamma,
                                                            const float* __restrict__ beta, int N,
                                                            float eps) {
-    __shared__ float red[4];
+    __shared__ float red[LT / 64];
     const float* x = in + (int64_t)blockIdx.x * N;
     float* y = out + (int64_t)blockIdx.x * N;
     float s = 0.0f;
     row_loop(N, [&](int j) { s += x[j]; });
-    const float mean = block_sum(s, red) / (float)N;
+    const float mean = group_sum<LT>(s, red) / (float)N;
     float q = 0.0f;
     row_loop(N, [&](int j) {
         const float d = x[j] - mean;
         q = __builtin_fmaf(d, d, q);
     });
-    const float var = block_sum(q, red) / (float)N;
+    const float var = group_sum<LT>(q, red) / (float)N;
     const float inv_std = 1.0f / sqrtf(var + eps);
     row_loop(N, [&](int j) { y[j] = __builtin_fmaf((x[j] - mean) * inv_std, gamma[j], beta[j]); });
 }
 
 // ---- cross entropy: grad rows and per-row losses (row_loss[M]) ----
 // A target outside [0, N) gives a NaN row loss and no onehot subtraction
-// (the reference indexes out of bounds).
-__device__ __forceinline__ float ce_grad(float p, int j, int t, float fm) {
-    return (j == t ? p - 1.0f : p) / fm;
-}
-
-template <int ELEMS>
-__global__ __launch_bounds__(256) void cross_entropy_kernel(const float* __restrict__ logits,
-                                                            const int32_t* __restrict__ targets,
-                                                            float* __restrict__ grad,
-                                                            float* __restrict__ row_loss, int M,
-                                                            int N) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+// (the reference indexes out of bounds).  p[t] is recomputed from x[t] with
+// the same operations as the row's own p (one cached load per row), and
+// grad[t] is stored again after the row with the onehot subtracted (the
+// same thread's later store to the same address wins).
+template <int G, int ELEMS, bool VEC, bool FULL>
+__global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void cross_entropy_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ targets,
+    float* __restrict__ grad, float* __restrict__ row_loss, int M, int N) {
+    __shared__ float red[G == 64 ? 1 : G / 64];
+    int tid;
+    const int row = held_row<G>(&tid);
     if (row >= M) return;
     const float* x = logits + (int64_t)row * N;
     float* g = grad + (int64_t)row * N;
-    float v[ELEMS];
-    softmax_cached<ELEMS>(v, x, N, lane);
     const int t = targets[row];
     const bool valid = t >= 0 && t < N;
-    // p[t]: held by lane t % 64 in slot t / 64
-    float pt = 0.0f;
-#pragma unroll
-    for (int k = 0; k < ELEMS; ++k)
-        if (lane + 64 * k == t) pt = v[k];
-    pt = wave_sum(pt);  // one lane holds it, the others 0
+    // the thread whose elements include t; it reads x[t] before any store of
+    // this row (grad may alias logits)
+    const bool owner = valid && tid == (VEC ? (t >> 2) % G : t % G);
+    const float xt = owner ? x[t] : 0.0f;
+    RowRegs<G, ELEMS, VEC> R;
+    float mx, s;
+    softmax_held<FULL>(R, x, N, tid, red, &mx, &s);
+    const int nv = N & ~15;
+    const float pt = row_norm(row_exp(xt - mx, t, nv), 1.0f / s, s, t, nv);
     const float fm = (float)M;
 #pragma unroll
-    for (int k = 0; k < ELEMS; ++k) {
-        const int j = lane + 64 * k;
-        if (j < N) g[j] = ce_grad(v[k], j, valid ? t : -1, fm);
+    for (int k = 0; k < ELEMS; ++k) R.v[k] = R.v[k] / fm;
+    R.store(g, N, tid);
+    if (owner) {
+        g[t] = (pt - 1.0f) / fm;  // after this thread's own store of g[t]
+        row_loss[row] = -logf(pt + 1e-10f);
+    } else if (!valid && tid == 0) {
+        row_loss[row] = __builtin_nanf("");
     }
-    if (lane == 0) row_loss[row] = valid ? -logf(pt + 1e-10f) : __builtin_nanf("");
 }
 
 __global__ __launch_bounds__(LT) void cross_entropy_long_kernel(const float* logits,
                                                                const int32_t* targets, float* grad,
                                                                float* row_loss, int M, int N) {
-    __shared__ float red[4];
+    __shared__ float red[LT / 64];
     const int row = blockIdx.x;
     const float* x = logits + (int64_t)row * N;
     float* g = grad + (int64_t)row * N;
     const int nv = N & ~15;
     float mx, s;
-    long_row_stats(x, N, red, &mx, &s);
-    const float inv = 1.0f / s;
     const int t = targets[row];
     const bool valid = t >= 0 && t < N;
+    const bool owner = valid && (int)threadIdx.x == t % LT;  // row_loop's owner of element t
+    const float xt = owner ? x[t] : 0.0f;  // before any store of this row (grad may alias logits)
+    long_row_stats(x, N, red, &mx, &s);
+    const float inv = 1.0f / s;
     const float fm = (float)M;
-    float pt = 0.0f;
-    row_loop(N, [&](int j) {
-        const float p = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv);
-        if (j == t) pt = p;
-        g[j] = ce_grad(p, j, valid ? t : -1, fm);
-    });
-    pt = block_sum(pt, red);  // one thread holds it, the others 0
-    if (threadIdx.x == 0) row_loss[row] = valid ? -logf(pt + 1e-10f) : __builtin_nanf("");
+    row_loop(N, [&](int j) { g[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv) / fm; });
+    if (owner) {
+        const float pt = row_norm(row_exp(xt - mx, t, nv), inv, s, t, nv);
+        g[t] = (pt - 1.0f) / fm;  // after this thread's own store of g[t]
+        row_loss[row] = -logf(pt + 1e-10f);
+    } else if (!valid && threadIdx.x == 0) {
+        row_loss[row] = __builtin_nanf("");
+    }
 }
 
 // loss = sum of row_loss in a fixed order / M (one workgroup)
@@ -287,43 +398,84 @@ __global__ __launch_bounds__(256) void cross_entropy_reduce_kernel(const float* 
     if (threadIdx.x == 0) loss[0] = ((part[0] + part[1]) + (part[2] + part[3])) / (float)M;
 }
 
-// one wave per row: the smallest register-cache size that holds N
+// Launch plan for a row length: the smallest register-held size that fits
+// (one wave per row up to MAX_CACHED, one BT-thread block per row up to
+// MAX_BLOCK_CACHED), 16-byte accesses when every row is 16-byte aligned, the
+// no-tail softmax when N % 16 == 0.  f(G, ELEMS, VEC, FULL) returns the
+// launch status; rows past MAX_BLOCK_CACHED are left to the caller
+// (streaming kernels).
+template <int G, int E, typename F>
+hipError_t with_flags(bool vec, bool full, F&& f) {
+    using std::integral_constant;
+    using g = integral_constant<int, G>;
+    using e = integral_constant<int, E>;
+    if constexpr (E < 4) {
+        return full ? f(g{}, e{}, integral_constant<bool, false>{}, integral_constant<bool, true>{})
+                    : f(g{}, e{}, integral_constant<bool, false>{}, integral_constant<bool, false>{});
+    } else {
+        if (vec)
+            return full ? f(g{}, e{}, integral_constant<bool, true>{}, integral_constant<bool, true>{})
+                        : f(g{}, e{}, integral_constant<bool, true>{}, integral_constant<bool, false>{});
+        return full ? f(g{}, e{}, integral_constant<bool, false>{}, integral_constant<bool, true>{})
+                    : f(g{}, e{}, integral_constant<bool, false>{}, integral_constant<bool, false>{});
+    }
+}
 template <typename F>
-hipError_t by_elems(int N, F&& f) {
-    if (N <= 64) return f(std::integral_constant<int, 1>{});
-    if (N <= 128) return f(std::integral_constant<int, 2>{});
-    if (N <= 256) return f(std::integral_constant<int, 4>{});
-    if (N <= 512) return f(std::integral_constant<int, 8>{});
-    if (N <= 1024) return f(std::integral_constant<int, 16>{});
-    if (N <= 2048) return f(std::integral_constant<int, 32>{});
-    return f(std::integral_constant<int, 64>{});
+hipError_t by_size(int N, bool vec, F&& f) {
+    const bool full = N % 16 == 0;
+    if (N <= 64) return with_flags<64, 1>(vec, full, f);
+    if (N <= 128) return with_flags<64, 2>(vec, full, f);
+    if (N <= 256) return with_flags<64, 4>(vec, full, f);
+    if (N <= 512) return with_flags<64, 8>(vec, full, f);
+    if (N <= 1024) return with_flags<64, 16>(vec, full, f);
+    if (N <= 2048) return with_flags<64, 32>(vec, full, f);
+    if (N <= 4096) return with_flags<64, 64>(vec, full, f);
+    if (N <= 8192) return with_flags<BT, 8>(vec, full, f);
+    if (N <= 16384) return with_flags<BT, 16>(vec, full, f);
+    return with_flags<BT, 32>(vec, full, f);
+}
+
+bool rows_vec4(int N, std::initializer_list<const void*> ptrs) {
+    if (N % 4 != 0) return false;
+    for (const void* p : ptrs)
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+    return true;
+}
+
+template <int G>
+unsigned row_blocks(int M) {
+    return G == 64 ? (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK) : (unsigned)M;
 }
 
 }  // namespace
 
 hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t s) {
-    const unsigned blocks = (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
-    if (N > MAX_CACHED) {
+    if (M == 0) return hipSuccess;
+    if (N > MAX_BLOCK_CACHED) {
         hipLaunchKernelGGL(softmax_long_kernel, dim3(M), dim3(LT), 0, s, out, in, N);
         return hipGetLastError();
     }
-    return by_elems(N, [&](auto e) {
-        hipLaunchKernelGGL(softmax_kernel<decltype(e)::value>, dim3(blocks), dim3(256), 0, s, out,
-                           in, M, N);
+    return by_size(N, rows_vec4(N, {out, in}), [&](auto g, auto e, auto v, auto f) {
+        constexpr int G = decltype(g)::value;
+        hipLaunchKernelGGL((softmax_kernel<G, decltype(e)::value, decltype(v)::value, decltype(f)::value>),
+                           dim3(row_blocks<G>(M)), dim3(G == 64 ? 64 * ROWS_PER_BLOCK : BT), 0, s,
+                           out, in, M, N);
         return hipGetLastError();
     });
 }
 
 hipError_t launch_layernorm(float* out, const float* in, const float* gamma, const float* beta,
                             int M, int N, float eps, hipStream_t s) {
-    const unsigned blocks = (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
-    if (N > MAX_CACHED) {
+    if (M == 0) return hipSuccess;
+    if (N > MAX_BLOCK_CACHED) {
         hipLaunchKernelGGL(layernorm_long_kernel, dim3(M), dim3(LT), 0, s, out, in, gamma, beta, N,
                            eps);
         return hipGetLastError();
     }
-    return by_elems(N, [&](auto e) {
-        hipLaunchKernelGGL(layernorm_kernel<decltype(e)::value>, dim3(blocks), dim3(256), 0, s,
+    return by_size(N, rows_vec4(N, {out, in, gamma, beta}), [&](auto g, auto e, auto v, auto) {
+        constexpr int G = decltype(g)::value;
+        hipLaunchKernelGGL((layernorm_kernel<G, decltype(e)::value, decltype(v)::value, false>),
+                           dim3(row_blocks<G>(M)), dim3(G == 64 ? 64 * ROWS_PER_BLOCK : BT), 0, s,
                            out, in, gamma, beta, M, N, eps);
         return hipGetLastError();
     });
@@ -331,19 +483,22 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
 
 hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, float* grad,
                                 float* loss, float* row_loss, int M, int N, hipStream_t s) {
-    const unsigned blocks = (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
-    hipError_t e;
-    if (N > MAX_CACHED) {
-        if (M > 0)
+    hipError_t e = hipSuccess;
+    if (M > 0) {
+        if (N > MAX_BLOCK_CACHED) {
             hipLaunchKernelGGL(cross_entropy_long_kernel, dim3(M), dim3(LT), 0, s, logits, targets,
                                grad, row_loss, M, N);
-        e = hipGetLastError();
-    } else {
-        e = by_elems(N, [&](auto el) {
-            hipLaunchKernelGGL(cross_entropy_kernel<decltype(el)::value>, dim3(blocks), dim3(256), 0,
-                               s, logits, targets, grad, row_loss, M, N);
-            return hipGetLastError();
-        });
+            e = hipGetLastError();
+        } else {
+            e = by_size(N, rows_vec4(N, {logits, grad}), [&](auto g, auto el, auto v, auto f) {
+                constexpr int G = decltype(g)::value;
+                hipLaunchKernelGGL((cross_entropy_kernel<G, decltype(el)::value, decltype(v)::value,
+                                                         decltype(f)::value>),
+                                   dim3(row_blocks<G>(M)), dim3(G == 64 ? 64 * ROWS_PER_BLOCK : BT), 0,
+                                   s, logits, targets, grad, row_loss, M, N);
+                return hipGetLastError();
+            });
+        }
     }
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(cross_entropy_reduce_kernel, dim3(1), dim3(256), 0, s, row_loss, loss, M);

@@ -8,7 +8,9 @@ order instead of the reference's 16 lane partials).  Shapes cover the
 reference's own benchmark shapes (softmax [64,256], [64,10], [2048,2048];
 layernorm [64,256], [2048,256]), the 16-element vector/tail split (N = 15,
 16, 17, 33), N = 1, ragged M, rows held in registers at every cache size,
-and rows longer than 4096 (the streaming passes)."""
+rows of 4097-32768 held by one 1024-thread block (16-byte and 4-byte
+accesses), rows longer than 32768 (the streaming passes), rows that are not
+16-byte aligned (the 4-byte path) and an in-place cross entropy."""
 import numpy as np
 import pytest
 import torch
@@ -21,7 +23,8 @@ from tests.helpers import case, registry_call, to_dev, to_np
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(64, 256), (64, 10), (2048, 2048), (2048, 256), (1, 1), (3, 15), (5, 16), (7, 17),
-          (9, 33), (13, 100), (6, 600), (5, 1500), (3, 4000), (3, 4096), (2, 4097), (2, 10000)]
+          (9, 33), (13, 100), (6, 600), (5, 1500), (3, 4000), (3, 4096), (2, 4097), (2, 10000),
+          (3, 16386), (2, 20001), (2, 32768), (2, 32769), (2, 40000)]
 
 
 def _x(M, N, seed, scale=3.0):
@@ -82,7 +85,7 @@ def test_layernorm_epsilon_and_constant_rows(dev):
 
 
 @pytest.mark.parametrize("M,N", [(64, 10), (128, 1000), (7, 17), (1, 1), (5, 4096), (3, 7000),
-                                 (2048, 512)])
+                                 (2048, 512), (3, 32000), (2, 20001), (2, 40000)])
 def test_cross_entropy(dev, M, N):
     case(f"cross entropy [{M},{N}]")
     x = _x(M, N, 3 * M + N)
@@ -114,6 +117,36 @@ def test_cross_entropy_bad_target_and_repeat(dev):
     assert float(to_np(l1)[0]) == float(to_np(l3)[0])
     # the bad row's gradient is the plain softmax / M (no onehot subtraction)
     np.testing.assert_allclose(to_np(g2)[2], po.softmax(x)[2] / 6, rtol=2e-6)
+
+
+@pytest.mark.parametrize("N", [256, 2048, 8192])
+def test_unaligned_rows_and_in_place(dev, N):
+    """Rows whose start is only 4-byte aligned take the 4-byte path (same
+    results); cross entropy with grad written over the logits."""
+    case(f"row kernels unaligned, in place N={N}")
+    M = 5
+    x = _x(M, N, N + 1)
+    flat = torch.empty((M * N + 1,), dtype=torch.float32, device=dev)
+    xs = flat[1:].view(M, N)
+    xs.copy_(to_dev(x, torch.float32, dev))
+    assert xs.data_ptr() % 16 != 0
+    y = to_np(ops.softmax(xs, out=torch.empty_like(xs)))
+    assert I.rel_err(y, po.softmax(x)) < 2e-6
+    g = np.linspace(-1, 1, N).astype(np.float32)
+    b = np.linspace(2, 0, N).astype(np.float32)
+    gf = torch.empty((N + 1,), dtype=torch.float32, device=dev)
+    gs = gf[1:]
+    gs.copy_(to_dev(g, torch.float32, dev))
+    y = to_np(ops.layernorm(xs, gs, to_dev(b, torch.float32, dev), eps=1e-5))
+    assert I.rel_err(y, po.layernorm64(x, g, b, 1e-5)) < I.TOL["f32"]
+    t = np.random.default_rng(N).integers(0, N, M).astype(np.int32)
+    lr, gr = po.cross_entropy(x, t)
+    loss, gg = ops.cross_entropy(xs, to_dev(t, torch.int32, dev), grad=xs)  # in place, unaligned
+    assert I.rel_err(to_np(gg), gr) < 2e-6
+    assert abs(float(to_np(loss)[0]) - lr) <= 2e-6 * max(1.0, abs(lr))
+    xa = to_dev(x, torch.float32, dev)
+    loss, gg = ops.cross_entropy(xa, to_dev(t, torch.int32, dev), grad=xa)  # in place, aligned
+    assert I.rel_err(to_np(gg), gr) < 2e-6
 
 
 def test_registry_row_kernels(dev):
