@@ -172,7 +172,12 @@ def test_registry_path(dev):
 
 
 # ---- matmulInt8 ---------------------------------------------------------------
-@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (8, 33, 70), (64, 64, 64), (130, 200, 515)])
+# Paths: rows not 16-byte aligned (K or N % 16 != 0) take the SIMT kernel;
+# M <= 16 the streaming split-K kernel with integer atomics; larger M the
+# 32x32x32 MFMA tiles (ragged M/N edges, K tails of a 64-row slice).
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (8, 33, 70), (64, 64, 64), (130, 200, 515),
+                                   (1, 256, 64), (5, 48, 16), (8, 8192, 8192), (16, 4096, 1040),
+                                   (17, 144, 80), (200, 272, 144), (512, 768, 1024)])
 def test_int8_bit_exact(dev, M, N, K):
     case(f"matmulInt8 {M}x{N}x{K}")
     A = I.int8_uniform(1, 0, (M, K))
@@ -182,6 +187,21 @@ def test_int8_bit_exact(dev, M, N, K):
         y = ops.matmul_int8(to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev), 0.013, 0.021,
                             None if b is None else to_dev(b, torch.float32, dev))
         np.testing.assert_array_equal(to_np(y), po.matmul_int8(A, B, 0.013, 0.021, b))
+
+
+@pytest.mark.parametrize("M", [2, 40])
+def test_int8_extreme_sums(dev, M):
+    """K = 131072 (the largest K the entry point accepts) with every product
+    127 * -128: |sum| = 2,130,706,432, just inside int32; the split-K partials
+    and their atomic combination stay exact."""
+    case(f"matmulInt8 extreme sums M={M}")
+    K, N = 131072, 16
+    A = np.full((M, K), 127, np.int8)
+    B = np.full((K, N), -128, np.int8)
+    B[:, 3] = 127
+    y = to_np(ops.matmul_int8(to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev), 1.0, 1.0))
+    np.testing.assert_array_equal(y, po.matmul_int8(A, B, 1.0, 1.0))
+    assert y[0, 0] == np.float32(-127 * 128 * K) and y[0, 3] == np.float32(127 * 127 * K)
 
 
 def test_int8_one_hot_kat(dev):
