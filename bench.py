@@ -11,7 +11,8 @@ The same run also times every BASELINE config on its own (per_config, keys
 c1-c5), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
 entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
 (per_config, keys m1-m2, fp32 TFLOP/s), the flash-attention backward at C4's
-shape (per_config, key b4), the dominant kernel against its roofline
+shape (per_config, key b4), matmulInt8 (per_config, keys i1-i2: int8 TOP/s at
+4096^3, GB/s at the decode shape), the dominant kernel against its roofline
 (roofline), and the CPU port of the reference AVX-512 path on a bounded
 sample (cpu_baseline).
 
@@ -28,7 +29,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "fused GEMM & flash-attn fwd TFLOP/s on 1 MI355X; % of MFMA/HBM roofline"
-PEAK = {"bf16": 2516.6, "f32": 157.3, "hbm": 8000.0}  # TFLOP/s, TFLOP/s, GB/s
+# TFLOP/s, TFLOP/s, GB/s, TOP/s (int8 dense: twice the bf16 rate, the published 5.0 POP/s)
+PEAK = {"bf16": 2516.6, "f32": 157.3, "hbm": 8000.0, "int8": 5033.2}
 
 
 # HBM bytes per launch of each config's kernel(s), measured with rocprofv3
@@ -89,6 +91,16 @@ MLP_CONFIGS = {
 # and the recomputed S: five products against the forward's two).
 BWD_CONFIGS = {
     "b4": dict(kind="flash_bwd", dtype="bf16", B=8, H=32, S=4096, D=128, causal=True),
+}
+
+
+# matmulInt8 (FusedKernels.h:867; a hot-path function with no BASELINE
+# config): a square MFMA-tile shape, and the decode shape of C5 with int8
+# activations (the reference benchmark's own matmulInt8 case in SURVEY's
+# CPU-baseline plan), weights rotated through HBM like C5.
+INT8_CONFIGS = {
+    "i1": dict(kind="int8", M=4096, N=4096, K=4096),
+    "i2": dict(kind="int8", M=8, N=8192, K=8192),
 }
 
 
@@ -178,6 +190,22 @@ class Runner:
             self.ws = ops.mlp_workspace(M, K1, N1, N2, dev)
             self.work = mlp_flops(s)
             self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK["f32"]
+        elif s["kind"] == "int8":
+            M, N, K = s["M"], s["N"], s["K"]
+            rnd = lambda *shape: torch.randint(-127, 128, shape, generator=g, device=dev,
+                                               dtype=torch.int8)
+            self.A = rnd(M, K)
+            # decode shapes stream B from HBM: rotate buffers past the MALL
+            self.nw = 8 if M <= 16 else 1
+            self.W = [rnd(K, N) for _ in range(self.nw)]
+            self.bias = torch.rand((N,), generator=g, device=dev) * 0.2 - 0.1
+            self.C = torch.empty((M, N), device=dev)
+            if M <= 16:
+                self.work = float(M * K + K * N + 4 * M * N + 4 * N)
+                self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK["hbm"]
+            else:
+                self.work = 2.0 * M * N * K
+                self.unit, self.bound, self.peak = "TOP/s", "mfma", PEAK["int8"]
         else:
             M, N, K = s["M"], s["N"], s["K"]
             # 64 MiB of weights fits in the 256 MB MALL: rotate 8 distinct
@@ -213,6 +241,9 @@ class Runner:
             self.out = ops.mlp_forward_backward(self.X, self.W1, self.b1, self.W2, self.b2, self.t,
                                                 with_dX=True, workspace=self.ws,
                                                 out=getattr(self, "out", None))
+        elif s["kind"] == "int8":
+            ops.matmul_int8(self.A, self.W[self.i % self.nw], 0.013, 0.021, self.bias, out=self.C)
+            self.i += 1
         else:
             ops.w8a16_gemm(self.x, self.W[self.i % self.nw], self.scale, self.bias, s["act"],
                            out=self.y, workspace=self.ws)
@@ -220,7 +251,7 @@ class Runner:
 
     def rate(self, ms):
         """work per launch / launch duration, in the config's unit"""
-        return self.work / (ms * 1e-3) / 1e12 if self.unit == "TFLOP/s" else self.work / (ms * 1e-3) / 1e9
+        return self.work / (ms * 1e-3) / (1e9 if self.unit == "GB/s" else 1e12)
 
 
 class CeilingRunner:
@@ -394,7 +425,7 @@ def main():
 
     # ---- per-config launch timings -----------------------------------------
     per = {}
-    ALL = {**CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS}
+    ALL = {**CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS, **INT8_CONFIGS}
     names = [n for n in ALL if not args.only or n in args.only.split(",")]
     if args.step_only:
         names = []

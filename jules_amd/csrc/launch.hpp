@@ -23,6 +23,12 @@ hipError_t launch_flash_bwd(int dtype, int causal, float scale, const void* Q, c
                             void* dQ, void* dK, void* dV, int B, int H, int S, int D, void* ws,
                             hipStream_t s);
 size_t w8a16_workspace_size(int M, int N, int K);
+// int8 x int8 at M <= 16 with the W8A16 split-K design (w8a16.hip); K and N
+// multiples of 16, A and B 16-byte aligned
+size_t int8_decode_workspace_size(int M, int N, int K);
+hipError_t launch_int8_decode(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
+                              float scale_a, float scale_b, const float* row_scale,
+                              const float* col_scale, const float* bias, void* ws, hipStream_t s);
 hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float* scale,
                         const float* bias, uint16_t* y, int M, int N, int K, void* ws,
                         hipStream_t s);

@@ -12,16 +12,12 @@
 // int8 MFMAs want K contiguous in every lane for both operands; A has it, B
 // is transposed on the way:
 //
-// Decode shapes (M <= 16): HBM-bound, the design of the W8A16 kernel.  Each
-// lane loads 16 consecutive columns of 16 consecutive B rows with 16-byte
-// loads, transposes the 16x16 bytes in registers (v_perm_b32, 4x4 blocks)
-// and feeds each column as the B operand of v_mfma_i32_16x16x64_i8 with A as
-// the A operand (M padded to 16).  A workgroup owns 256 columns and one of KS
-// K-ranges; the 8 wave partials are summed in LDS and the workgroup adds its
-// exact int32 partial tile into C, used as int32 scratch, with integer
-// atomics (order-free, so the result is deterministic).  C is zeroed before
-// and converted in place after (C = float(sum) * scale + bias), three
-// launches in all and no workspace.
+// Decode shapes (M <= 16): HBM-bound, the W8A16 kernel's design with integer
+// arithmetic (int8_splitk_kernel in w8a16.hip): 16-byte loads of B rows, a
+// 16x16 byte transpose in registers, v_mfma_i32_16x16x64_i8, exact int32
+// split-K partials summed in split order by the last workgroup of each
+// column tile, one launch.  The entry point has no workspace argument, so the
+// library keeps one per (device, stream).
 //
 // Larger M: v_mfma_i32_32x32x32_i8 on 128x128 tiles, 4 waves of 64x64, K in
 // slices of 64 staged through double-buffered LDS (next slice in registers
@@ -32,6 +28,9 @@
 //
 // Shapes whose rows are not 16-byte aligned (K or N not a multiple of 16, or
 // misaligned pointers) take a plain LDS-tiled SIMT kernel.
+#include <map>
+#include <mutex>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -106,145 +105,6 @@ __device__ __forceinline__ float int8_epilogue(int sum, int m, int n, float scal
     float c = (float)sum * sc;
     if (bias) c = c + bias[n];
     return c;
-}
-
-// ---------------------------------------------------------------------------
-// Decode shapes (M <= 16)
-// ---------------------------------------------------------------------------
-constexpr int DCOLS = 256;      // columns per workgroup: 16 lanes x 16 columns
-constexpr int DWAVES = 8;
-constexpr int DTHREADS = DWAVES * 64;
-constexpr int DKSTEP = 64;      // rows per MFMA k-step
-constexpr int DMAX_KS = 8;
-
-struct DPlan {
-    int ks;     // K splits
-    int steps;  // k-steps per wave
-};
-inline DPlan dplan(int K, int N) {
-    const int total = (K + DKSTEP - 1) / DKSTEP;
-    const int tiles = (N + DCOLS - 1) / DCOLS;
-    // about 256 workgroups in all, at least two k-steps per wave
-    int ks = (256 + tiles - 1) / tiles;
-    const int max_ks = (total + 2 * DWAVES - 1) / (2 * DWAVES);
-    if (ks > max_ks) ks = max_ks;
-    if (ks > DMAX_KS) ks = DMAX_KS;
-    if (ks < 1) ks = 1;
-    const int per_split = (total + ks - 1) / ks;
-    return {ks, (per_split + DWAVES - 1) / DWAVES};
-}
-
-// 4x4 byte transpose: rows a, b, c, e (4 column bytes each) -> t[j] = byte j
-// of a, b, c, e (one column's 4 rows)
-__device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t e,
-                                             uint32_t (&t)[4]) {
-    // v_perm_b32(s0, s1, sel): byte i of the result = byte sel_i of {s0:s1}
-    // (0-3 select s1, 4-7 select s0)
-    const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
-    const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
-    const uint32_t ce_lo = __builtin_amdgcn_perm(e, c, 0x05010400u);  // c0 e0 c1 e1
-    const uint32_t ce_hi = __builtin_amdgcn_perm(e, c, 0x07030602u);  // c2 e2 c3 e3
-    t[0] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x05040100u);         // a0 b0 c0 e0
-    t[1] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x07060302u);         // a1 b1 c1 e1
-    t[2] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x05040100u);
-    t[3] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x07060302u);
-}
-
-__global__ void int8_zero_kernel(int* __restrict__ c, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) c[i] = 0;
-}
-
-__global__ __launch_bounds__(DTHREADS, 1) void int8_decode_kernel(
-    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int* __restrict__ Ci, int M, int N,
-    int K, int KS, int steps) {
-    __shared__ i32x4_t red[DWAVES * 16 * 64];  // 128 KiB: [wave][j][lane]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile = blockIdx.x, split = blockIdx.y;
-    const int n0 = tile * DCOLS;
-    const int lc = lane & 15, lg = lane >> 4;  // column chunk, k group
-    const int col0 = n0 + 16 * lc;             // this lane's 16 columns
-    const bool col_ok = col0 < N;
-
-    i32x4_t acc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = i32x4_t{0, 0, 0, 0};
-
-    const int total = (K + DKSTEP - 1) / DKSTEP;
-    const int per_split = (total + KS - 1) / KS;
-    const int s0 = split * per_split;
-    const int s1 = min(total, s0 + per_split);
-
-    for (int t = 0; t < steps; ++t) {
-        const int st = s0 + wave + DWAVES * t;
-        if (st >= s1) break;  // wave-uniform
-        const int kb = st * DKSTEP + 16 * lg;  // this lane's 16 rows
-        // branch-free loads: an out-of-range row reads row 0 and is replaced by zeros
-        u32x4_t wr[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const bool ok = col_ok && kb + r < K;
-            const int64_t off = ok ? (int64_t)(kb + r) * N + col0 : 0;
-            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(B + off));
-            const u32x4_t z = {0u, 0u, 0u, 0u};
-            wr[r] = ok ? v : z;
-        }
-        // A operand: A[m = lane & 15][kb .. kb+15] (zero past M and K; K % 16 == 0)
-        const bool aok = lc < M && kb < K;
-        const u32x4_t av = *reinterpret_cast<const u32x4_t*>(A + (aok ? (int64_t)lc * K + kb : 0));
-        const u32x4_t z = {0u, 0u, 0u, 0u};
-        const i32x4_t a = __builtin_bit_cast(i32x4_t, aok ? av : z);
-        // column j = 4q + jj of the 16: byte jj of dword q of the 16 rows
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t col[4][4];  // [jj][row block d]
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                uint32_t t4[4];
-                transpose4x4(wr[4 * d][q], wr[4 * d + 1][q], wr[4 * d + 2][q], wr[4 * d + 3][q], t4);
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) col[jj][d] = t4[jj];
-            }
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const i32x4_t b = {(int)col[jj][0], (int)col[jj][1], (int)col[jj][2], (int)col[jj][3]};
-                acc[4 * q + jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[4 * q + jj], 0, 0, 0);
-            }
-        }
-    }
-
-    // ---- 8 wave partials summed in LDS; wave w then owns accumulators
-    // j = 2w, 2w+1 (lane (lc, lg): rows 4 lg .. 4 lg + 3 of column n0 + 16 lc + j) ----
-#pragma unroll
-    for (int j = 0; j < 16; ++j) red[(wave * 16 + j) * 64 + lane] = acc[j];
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int j = 2 * wave + h;
-        i32x4_t r = red[j * 64 + lane];
-#pragma unroll
-        for (int w = 1; w < DWAVES; ++w) r += red[(w * 16 + j) * 64 + lane];
-        const int c = n0 + 16 * lc + j;
-        if (c >= N) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * lg + i;
-            if (m < M)
-                __hip_atomic_fetch_add(Ci + (int64_t)m * N + c, r[i], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-}
-
-// C = float(sum) * scale + bias in place over the int32 sums
-__global__ void int8_finish_kernel(float* __restrict__ C, int M, int N, float scale_a,
-                                   float scale_b, const float* __restrict__ row_scale,
-                                   const float* __restrict__ col_scale, const float* __restrict__ bias) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)M * N) return;
-    const int m = (int)(i / N), n = (int)(i % N);
-    const int sum = __builtin_bit_cast(int, C[i]);
-    C[i] = int8_epilogue(sum, m, n, scale_a, scale_b, row_scale, col_scale, bias);
 }
 
 // ---------------------------------------------------------------------------
@@ -369,22 +229,42 @@ __global__ __launch_bounds__(256, 2) void int8_mfma_kernel(
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Workspace of the decode path, one per (device, stream) and kept for the
+// process: calls on one stream run in order and may share it, calls on other
+// streams get their own.  A larger need replaces it once the stream has
+// finished with the old one.
+hipError_t stream_workspace(size_t need, hipStream_t s, void** ws) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> cache;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    auto& slot = cache[{dev, s}];
+    if (slot.second < need) {
+        if (slot.first) {
+            if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+            (void)hipFree(slot.first);
+        }
+        slot = {nullptr, 0};
+        void* p = nullptr;
+        if ((e = hipMalloc(&p, need)) != hipSuccess) return e;
+        slot = {p, need};
+    }
+    *ws = slot.first;
+    return hipSuccess;
+}
+
 hipError_t launch_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                        float scale_a, float scale_b, const float* row_scale, const float* col_scale,
                        const float* bias, hipStream_t s) {
     if (M == 0 || N == 0) return hipSuccess;
     const bool vec = K > 0 && K % 16 == 0 && N % 16 == 0 && aligned16(A) && aligned16(B);
     if (vec && M <= 16) {
-        const int64_t mn = (int64_t)M * N;
-        int* Ci = reinterpret_cast<int*>(C);
-        hipLaunchKernelGGL(int8_zero_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, Ci, mn);
-        const DPlan p = dplan(K, N);
-        const int tiles = (N + DCOLS - 1) / DCOLS;
-        hipLaunchKernelGGL(int8_decode_kernel, dim3(tiles, p.ks), dim3(DTHREADS), 0, s, A, B, Ci, M,
-                           N, K, p.ks, p.steps);
-        hipLaunchKernelGGL(int8_finish_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, C,
-                           M, N, scale_a, scale_b, row_scale, col_scale, bias);
-        return hipGetLastError();
+        void* ws = nullptr;
+        const hipError_t e = stream_workspace(int8_decode_workspace_size(M, N, K), s, &ws);
+        if (e != hipSuccess) return e;
+        return launch_int8_decode(A, B, C, M, N, K, scale_a, scale_b, row_scale, col_scale, bias, ws, s);
     }
     if (vec) {
         const int nt = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);

@@ -281,6 +281,198 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// int8 x int8 at decode shapes (matmulInt8 / W8A8 with M <= 16): the same
+// streaming design and split-K reduction with exact integer arithmetic.
+// A lane loads 16 consecutive columns of 16 consecutive B rows, transposes
+// the 16x16 bytes in registers (v_perm_b32, 4x4 blocks) and feeds column j
+// as the B operand of v_mfma_i32_16x16x64_i8 with A (M padded to 16) as the
+// A operand.  Partials are int32 (exact for K <= 131072), summed in split
+// order by the last workgroup of the column tile, which applies the epilogue
+// C = float(sum) * (sA * sB) + bias of matmulInt8's scalar path.
+// ---------------------------------------------------------------------------
+constexpr int I8_KSTEP = 64;  // rows per int8 MFMA k-step
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+inline Plan plan_int8(int K) {
+    const int total_steps = (K + I8_KSTEP - 1) / I8_KSTEP;
+    // two k-steps per wave, at most MAX_KS splits (larger K: more k-steps per wave)
+    int ks = (total_steps + 2 * WAVES - 1) / (2 * WAVES);
+    if (ks > MAX_KS) ks = MAX_KS;
+    if (ks < 1) ks = 1;
+    const int per_split = (total_steps + ks - 1) / ks;
+    return {ks, (per_split + WAVES - 1) / WAVES};
+}
+
+// 4x4 byte transpose: rows a, b, c, e (4 column bytes each) -> t[j] = byte j
+// of a, b, c, e (one column's 4 rows)
+__device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t e,
+                                             uint32_t (&t)[4]) {
+    // v_perm_b32(s0, s1, sel): byte i of the result = byte sel_i of {s0:s1}
+    // (0-3 select s1, 4-7 select s0)
+    const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+    const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+    const uint32_t ce_lo = __builtin_amdgcn_perm(e, c, 0x05010400u);  // c0 e0 c1 e1
+    const uint32_t ce_hi = __builtin_amdgcn_perm(e, c, 0x07030602u);  // c2 e2 c3 e3
+    t[0] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x05040100u);         // a0 b0 c0 e0
+    t[1] = __builtin_amdgcn_perm(ce_lo, ab_lo, 0x07060302u);         // a1 b1 c1 e1
+    t[2] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x05040100u);
+    t[3] = __builtin_amdgcn_perm(ce_hi, ab_hi, 0x07060302u);
+}
+
+__global__ __launch_bounds__(THREADS, 1) void int8_splitk_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K, int KS,
+    int steps, float* __restrict__ partials, float scale_a, float scale_b,
+    const float* __restrict__ row_scale, const float* __restrict__ col_scale,
+    const float* __restrict__ bias, float* __restrict__ C, uint64_t* __restrict__ flags,
+    uint64_t call_id) {
+    __shared__ i32x4_t red[WAVES * 16 * 64];  // 128 KiB: [wave][j][lane]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = blockIdx.x, split = blockIdx.y;
+    const int n0 = tile * COLS;
+    const int lc = lane & 15, lg = lane >> 4;  // column chunk, k group
+    const int col0 = n0 + 16 * lc;             // this lane's 16 columns
+    const bool col_ok = col0 < N;
+
+    i32x4_t acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = i32x4_t{0, 0, 0, 0};
+
+    // epilogue operands of the two columns this lane finishes if its
+    // workgroup reduces the tile, loaded now (off the tail)
+    float csc[2], bi[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = min(n0 + 16 * lc + 2 * wave + h, N - 1);
+        csc[h] = col_scale ? col_scale[c] : scale_b;
+        bi[h] = bias ? bias[c] : 0.0f;
+    }
+
+    const int total_steps = (K + I8_KSTEP - 1) / I8_KSTEP;
+    const int per_split = (total_steps + KS - 1) / KS;
+    const int s0 = split * per_split;
+    const int s1 = min(total_steps, s0 + per_split);
+
+    for (int t = 0; t < steps; ++t) {
+        const int st = s0 + wave + WAVES * t;
+        const bool live = st < s1;
+        const int kb = st * I8_KSTEP + 16 * lg;  // this lane's 16 rows
+        // branch-free loads: an out-of-range row reads element 0 and is
+        // replaced by zeros (K % 16 == 0: a lane's rows are all in or all out)
+        u32x4_t wr[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const bool ok = live && col_ok && kb + r < K;
+            const int64_t off = ok ? (int64_t)(kb + r) * N + col0 : 0;
+            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(B + off));
+            const u32x4_t z = {0u, 0u, 0u, 0u};
+            wr[r] = ok ? v : z;
+        }
+        // A operand: A[m = lane & 15][kb .. kb+15]
+        const bool aok = live && lc < M && kb < K;
+        const u32x4_t av = *reinterpret_cast<const u32x4_t*>(A + (aok ? (int64_t)lc * K + kb : 0));
+        const u32x4_t z = {0u, 0u, 0u, 0u};
+        const i32x4_t a = __builtin_bit_cast(i32x4_t, aok ? av : z);
+        // column j = 4q + jj of the 16: byte jj of dword q of the 16 rows
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t col[4][4];  // [jj][row block d]
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                uint32_t t4[4];
+                transpose4x4(wr[4 * d][q], wr[4 * d + 1][q], wr[4 * d + 2][q], wr[4 * d + 3][q], t4);
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) col[jj][d] = t4[jj];
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const i32x4_t b = {(int)col[jj][0], (int)col[jj][1], (int)col[jj][2], (int)col[jj][3]};
+                acc[4 * q + jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[4 * q + jj], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- the 8 wave partials summed in LDS (wave w then owns j = 2w, 2w+1) ----
+#pragma unroll
+    for (int j = 0; j < 16; ++j) red[(wave * 16 + j) * 64 + lane] = acc[j];
+    lds_barrier();
+    i32x4_t r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int j = 2 * wave + h;
+        r[h] = red[j * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) r[h] += red[(w * 16 + j) * 64 + lane];
+    }
+
+    // ---- partial tile out, flags, the last workgroup reduces (the protocol
+    // of w8a16_splitk_kernel above) ----
+    const int tiles = gridDim.x;
+    const int lanes_live = 16 * ((M + 3) / 4);
+    const bool live = lane < lanes_live;
+    {
+        const __amdgpu_buffer_rsrc_t pr = part_rsrc(partials, split, tiles, tile, true);
+        if (live) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, r[h]), pr,
+                                                       ((2 * wave + h) * 64 + lane) * 16, 0, kSc1);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __shared__ int last;
+    lds_barrier();
+    if (wave == 0) {
+        uint64_t* tf = flags + (int64_t)tile * KS;
+        if (lane == 0) __hip_atomic_store(tf + split, call_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        const uint64_t f =
+            lane < KS ? __hip_atomic_load(tf + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : call_id;
+        const bool all = __builtin_amdgcn_ballot_w64(f != call_id) == 0;
+        if (lane == 0) last = all;
+    }
+    lds_barrier();
+    if (!last || !live) return;
+
+    i32x4_t pv[2][MAX_KS];
+#pragma unroll
+    for (int p = 0; p < MAX_KS; ++p) {
+        const __amdgpu_buffer_rsrc_t pr = part_rsrc(partials, p, tiles, tile, p < KS && p != split);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            pv[h][p] = __builtin_bit_cast(
+                i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(pr, ((2 * wave + h) * 64 + lane) * 16, 0, kSc1));
+    }
+#pragma unroll
+    for (int p = 0; p < MAX_KS; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(pv[h][p]));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = n0 + 16 * lc + 2 * wave + h;
+        i32x4_t sum = split == 0 ? r[h] : pv[h][0];
+#pragma unroll
+        for (int p = 1; p < MAX_KS; ++p) {
+            const i32x4_t v = p == split ? r[h] : pv[h][p];
+            if (p < KS) sum += v;
+        }
+        if (c >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * lg + i;
+            if (m < M) {
+                // the scale product rounded to fp32, one multiply, one add
+                const float sc = (row_scale ? row_scale[m] : scale_a) * csc[h];
+                float v = (float)sum[i] * sc;
+                if (bias) v = v + bi[h];
+                C[(int64_t)m * N + c] = v;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // workspace: KS x tiles partial tiles of PART_FLOATS fp32 each, then one
@@ -305,6 +497,27 @@ uint64_t next_call_id() {
     return start + counter.fetch_add(1, std::memory_order_relaxed) + 1;
 }
 }  // namespace
+
+// int8 decode workspace: the same layout with the int8 split plan
+size_t int8_decode_workspace_size(int M, int N, int K) {
+    (void)M;
+    const Plan p = plan_int8(K);
+    const size_t tiles = (size_t)(N + COLS - 1) / COLS;
+    return tiles * p.ks * (PART_FLOATS * sizeof(float) + sizeof(uint64_t));
+}
+
+hipError_t launch_int8_decode(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
+                              float scale_a, float scale_b, const float* row_scale,
+                              const float* col_scale, const float* bias, void* ws, hipStream_t s) {
+    const Plan p = plan_int8(K);
+    const int tiles = (N + COLS - 1) / COLS;
+    float* partials = static_cast<float*>(ws);
+    uint64_t* flags = reinterpret_cast<uint64_t*>(partials + (size_t)tiles * p.ks * PART_FLOATS);
+    hipLaunchKernelGGL(int8_splitk_kernel, dim3(tiles, p.ks), dim3(THREADS), 0, s, A, B, M, N, K, p.ks,
+                       p.steps, partials, scale_a, scale_b, row_scale, col_scale, bias, C, flags,
+                       next_call_id());
+    return hipGetLastError();
+}
 
 hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float* scale,
                         const float* bias, uint16_t* y, int M, int N, int K, void* ws,

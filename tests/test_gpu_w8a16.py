@@ -204,6 +204,30 @@ def test_int8_extreme_sums(dev, M):
     assert y[0, 0] == np.float32(-127 * 128 * K) and y[0, 3] == np.float32(127 * 127 * K)
 
 
+def test_int8_decode_two_streams(dev):
+    """The decode path's workspace is per (device, stream): calls alternating
+    on two streams, with inputs of two sizes (the workspace grows once), all
+    give the exact result."""
+    case("matmulInt8 decode on two streams")
+    ins = []
+    for i, (M, N, K) in enumerate([(8, 2048, 4096), (16, 4096, 8192)]):
+        A = I.int8_uniform(20 + i, 0, (M, K))
+        B = I.int8_uniform(20 + i, 1, (K, N))
+        ins.append((A, B, po.matmul_int8(A, B, 0.5, 0.25), to_dev(A, torch.int8, dev),
+                    to_dev(B, torch.int8, dev)))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    outs = []
+    for rep in range(6):
+        for si, st in enumerate(streams):
+            A, B, ref, tA, tB = ins[(rep + si) % 2]
+            with torch.cuda.stream(st):
+                outs.append((ops.matmul_int8(tA, tB, 0.5, 0.25), ref))
+    torch.cuda.synchronize()
+    for y, ref in outs:
+        np.testing.assert_array_equal(to_np(y), ref)
+
+
 def test_int8_one_hot_kat(dev):
     case("matmulInt8 one-hot KAT")
     B = I.int8_uniform(2, 1, (70, 40))
