@@ -26,8 +26,10 @@
 // 8-row x 16-column byte block and lane i receives column i).  Row strides
 // are padded so both reads are free of bank conflicts.
 //
-// Shapes whose rows are not 16-byte aligned (K or N not a multiple of 16, or
-// misaligned pointers) take a plain LDS-tiled SIMT kernel.
+// Full tiles (M, N multiples of 256, K of 64) take the bf16 GEMM's LDS-DMA
+// design instead (int8_dma_kernel below).  Shapes whose rows are not 16-byte
+// aligned (K or N not a multiple of 16, or misaligned pointers) take a plain
+// LDS-tiled SIMT kernel.
 #include <map>
 #include <mutex>
 
@@ -95,16 +97,6 @@ __global__ __launch_bounds__(256) void matmul_int8_simt_kernel(
             C[(int64_t)m * N + n] = c;
         }
     }
-}
-
-// the epilogue of one output element from its exact integer sum
-__device__ __forceinline__ float int8_epilogue(int sum, int m, int n, float scale_a, float scale_b,
-                                               const float* row_scale, const float* col_scale,
-                                               const float* bias) {
-    const float sc = (row_scale ? row_scale[m] : scale_a) * (col_scale ? col_scale[n] : scale_b);
-    float c = (float)sum * sc;
-    if (bias) c = c + bias[n];
-    return c;
 }
 
 // ---------------------------------------------------------------------------
@@ -210,9 +202,22 @@ __global__ __launch_bounds__(256, 2) void int8_mfma_kernel(
     }
 
     // epilogue: element e of acc[i][j] is row 8(e/4) + 4 kh + e%4 of the
-    // 32x32 tile, column fr
+    // 32x32 tile, column fr; per-column and per-row factors loaded once
+    float cs[2], bv[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j) {
+        const int n = min(n0 + wn * 64 + 32 * j + fr, N - 1);
+        cs[j] = col_scale ? col_scale[n] : scale_b;
+        bv[j] = bias ? bias[n] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        float rs[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int m = min(m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3), M - 1);
+            rs[e] = row_scale ? row_scale[m] : scale_a;
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int n = n0 + wn * 64 + 32 * j + fr;
@@ -220,11 +225,271 @@ __global__ __launch_bounds__(256, 2) void int8_mfma_kernel(
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int m = m0 + wm * 64 + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
-                if (m < M)
-                    C[(int64_t)m * N + n] =
-                        int8_epilogue(acc[i][j][e], m, n, scale_a, scale_b, row_scale, col_scale, bias);
+                if (m < M) {
+                    float c = (float)acc[i][j][e] * (rs[e] * cs[j]);
+                    if (bias) c = c + bv[j];
+                    C[(int64_t)m * N + n] = c;
+                }
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Full tiles (M, N multiples of 256, K of 64): the bf16 GEMM's LDS-DMA design
+// (gemm_bf16.hip) on v_mfma_i32_32x32x32_i8.  256x256 blocks, 4 waves of
+// 128x128 (4x4 MFMA tiles, 256 accumulators), K in slices of 64 through a
+// ring of 4 LDS stages filled by global_load_lds_dwordx4 (each lane's 16
+// bytes land at base + 16 * lane) three slices ahead, so the copies have two
+// to three slices of MFMA time to land.
+//   A stage: [256 rows][64 k] (64-byte rows), 16-byte chunk c of row r at
+//      c ^ ((r >> 2) & 3): a fragment read (16 rows, one chunk) touches 16
+//      distinct 16-byte bank groups.
+//   B stage: [64 k][256 n] (256-byte rows), 16-byte unit u of row r at
+//      u ^ 2 (r & 7).  A B fragment is two ds_read_b64_tr_b8 (rows +0..7 and
+//      +8..15 of the lane's 16 k); the two 16-lane groups served together
+//      read units u and u+1 (u even) of the same 8 rows, which the swizzle
+//      spreads over all 16 units of the 256-byte bank window.
+// Each lane's DMA source address is chosen so the data lands swizzled.  Per
+// 32-deep k-step a wave issues 4 ds_read_b128 and 8 ds_read_b64_tr_b8 for
+// 16 MFMAs, one read and (every fourth MFMA) one copy after each MFMA.
+// ---------------------------------------------------------------------------
+constexpr int QBK = 64;                // k per stage
+constexpr int QNSTAGE = 4;
+constexpr int QBM = 256, QBN = 256;
+constexpr int QTILE = 256 * QBK;       // one operand stage: 16 KiB
+constexpr int QSTAGE = 2 * QTILE;      // A then B
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ int qswz_a(int row, int chunk) {
+    return row * QBK + ((chunk ^ ((row >> 2) & 3)) << 4);
+}
+__device__ __forceinline__ int qswz_b(int row, int unit) {
+    return QTILE + row * QBN + ((unit ^ (2 * (row & 7))) << 4);
+}
+
+// LDS reads as inline asm (untracked by the compiler's wait-count pass,
+// which would otherwise drain every copy in flight before a transposed
+// read); lgkm_wait below orders their uses.
+__device__ __forceinline__ u32x2_t q_read_tr8(const uint8_t* p) {
+    u32x2_t v;
+    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(v) : "v"((uint32_t)(uintptr_t)p) : "memory");
+    return v;
+}
+__device__ __forceinline__ u32x4_t q_read_b128(const uint8_t* p) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"((uint32_t)(uintptr_t)p) : "memory");
+    return v;
+}
+
+struct QFrags {
+    u32x4_t a[4];
+    u32x4_t b[4];
+};
+// at most N LDS reads outstanding; the operands pass through the asm so no
+// MFMA that uses them is scheduled before it
+template <int N>
+__device__ __forceinline__ void q_lgkm_wait(QFrags& f) {
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.a[2]), "+v"(f.a[3]), "+v"(f.b[0]),
+                   "+v"(f.b[1]), "+v"(f.b[2]), "+v"(f.b[3])
+                 : "n"(N)
+                 : "memory");
+}
+
+__global__ __launch_bounds__(256, 1) void int8_dma_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, float* __restrict__ C, int M, int N,
+    int K, float scale_a, float scale_b, const float* __restrict__ row_scale,
+    const float* __restrict__ col_scale, const float* __restrict__ bias) {
+    __shared__ __attribute__((aligned(1024))) uint8_t sm[QNSTAGE * QSTAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    // XCD-aware order: each XCD gets a contiguous run of tiles, walked in
+    // groups of 4 row bands
+    const int tiles_m = M / QBM, tiles_n = N / QBN;
+    const int nblk = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if ((nblk & 7) == 0) t = (t & 7) * (nblk >> 3) + (t >> 3);
+    constexpr int GM = 4;
+    const int group = t / (GM * tiles_n);
+    const int first_m = group * GM;
+    const int gsize = min(GM, tiles_m - first_m);
+    const int tile_m = first_m + (t % (GM * tiles_n)) % gsize;
+    const int tile_n = (t % (GM * tiles_n)) / gsize;
+    const int m0 = tile_m * QBM, n0 = tile_n * QBN;
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+
+    // copy pieces: 16 A segments (16 rows x 64 B) and 16 B segments (4 rows x
+    // 256 B) of 1 KiB per slice; wave w moves segments w, w+4, w+8, w+12
+    const int8_t* a_src[4];
+    const int8_t* b_src[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int seg = i * 4 + wave_s;
+        const int row = seg * 16 + (lane >> 2);
+        const int lc = (lane & 3) ^ ((row >> 2) & 3);
+        a_src[i] = A + (int64_t)(m0 + row) * K + 16 * lc;
+        const int r = seg * 4 + (lane >> 4);
+        const int lu = (lane & 15) ^ (2 * (r & 7));
+        b_src[i] = B + (int64_t)r * N + n0 + 16 * lu;
+    }
+    auto dma_piece = [&](int stage, int kt, int q) {
+        uint8_t* st = sm + stage * QSTAGE;
+        const int i = q & 3;
+        const int seg = i * 4 + wave_s;
+        if (q < 4)
+            __builtin_amdgcn_global_load_lds(a_src[i] + kt * QBK, (lds_void*)(st + seg * 1024), 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(b_src[i] + (int64_t)kt * QBK * N,
+                                             (lds_void*)(st + QTILE + seg * 1024), 16, 0, 0);
+    };
+
+    i32x16_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = i32x16_t{};
+
+    const int wm = wave >> 1, wn = wave & 1;
+    const int frag_row = lane & 31, frag_half = lane >> 5;
+    const int ts = lane & 15, tdh = (lane >> 4) & 1;
+    // LDS offsets of the 12 reads of k-step ks: p < 4 the A fragment of
+    // m-tile p; p = 4 + 2 nt + h half h (rows +8h) of the B fragment of n-tile nt
+    auto piece_addr = [&](int ks, int p) -> int {
+        if (p < 4) return qswz_a(wm * 128 + p * 32 + frag_row, ks * 2 + frag_half);
+        const int nt = (p - 4) >> 1, h = (p - 4) & 1;
+        const int unit = (wn * 128 + nt * 32 + 16 * tdh) / 16;
+        const int r0 = 32 * ks + 16 * frag_half + 8 * h + (ts >> 1);
+        return qswz_b(r0, unit) + 8 * (ts & 1);
+    };
+    int off[2][12];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int p = 0; p < 12; ++p) off[ks][p] = piece_addr(ks, p);
+
+    auto read_piece = [&](QFrags& f, const uint8_t* stage_base, int ks, int p) {
+        const uint8_t* ptr = stage_base + off[ks][p];
+        if (p < 4) {
+            f.a[p] = q_read_b128(ptr);
+        } else {
+            const int nt = (p - 4) >> 1;
+            const u32x2_t v = q_read_tr8(ptr);
+            if ((p & 1) == 0) {
+                f.b[nt][0] = v[0];
+                f.b[nt][1] = v[1];
+            } else {
+                f.b[nt][2] = v[0];
+                f.b[nt][3] = v[1];
+            }
+        }
+    };
+    auto mfma1 = [&](const QFrags& f, int i) {
+        const int mt = i >> 2, nt = i & 3;
+        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, f.a[mt]),
+                                                           __builtin_bit_cast(i32x4_t, f.b[nt]),
+                                                           acc[mt][nt], 0, 0, 0);
+    };
+
+    // The software pipeline of the bf16 kernel: k-step 0 of slice kt runs
+    // its MFMAs with the reads of k-step 1 and copies 0-3 of slice kt+3;
+    // k-step 1 waits for slice kt+1 (vmcnt + bare barrier), runs its MFMAs
+    // with copies 4-7 of slice kt+3 and the reads of slice kt+1's k-step 0.
+    // Stage (kt+3)%4 = (kt-1)%4 was last read in k-step 0 of slice kt-1, and
+    // every wave passed the barrier of slice kt-1 after those reads completed.
+    const int KT = K / QBK;
+    auto wait_slice = [&](int outstanding) {
+        if (outstanding >= 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (outstanding >= 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        else if (outstanding >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else if (outstanding >= 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+    };
+    QFrags fr[2];
+    auto slice = [&](int kt, auto with_dma, auto with_next) {
+        constexpr bool DMA = decltype(with_dma)::value;
+        constexpr bool NEXT = decltype(with_next)::value;
+        const uint8_t* cur = sm + (kt % QNSTAGE) * QSTAGE;
+        const int dst = (kt + QNSTAGE - 1) % QNSTAGE;
+        QFrags& f0 = fr[0];
+        QFrags& f1 = fr[1];
+        q_lgkm_wait<0>(f0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            mfma1(f0, i);
+            if (i < 12) read_piece(f1, cur, 1, i);
+            if constexpr (DMA)
+                if ((i & 3) == 1) dma_piece(dst, kt + QNSTAGE - 1, i >> 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        q_lgkm_wait<0>(f1);
+        mfma1(f1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // issued after slice kt+1: slice kt+2 if it exists (8), and the first
+        // half of slice kt+3 (4)
+        if constexpr (NEXT) wait_slice((kt + 2 < KT ? 8 : 0) + (DMA ? 4 : 0));
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* nxt = sm + ((kt + 1) % QNSTAGE) * QSTAGE;
+#pragma unroll
+        for (int i = 1; i < 16; ++i) {
+            mfma1(f1, i);
+            if constexpr (NEXT)
+                if (i <= 12) read_piece(f0, nxt, 0, i - 1);
+            if constexpr (DMA)
+                if ((i & 3) == 3) dma_piece(dst, kt + QNSTAGE - 1, 4 + (i >> 2));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // prologue: slices 0..2 into stages 0..2 (stage 3 is filled during slice 0)
+#pragma unroll
+    for (int p = 0; p < QNSTAGE - 1; ++p)
+        if (p < KT)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) dma_piece(p, p, q);
+    wait_slice(8 * min(KT - 1, QNSTAGE - 2));
+#pragma unroll
+    for (int p = 0; p < 12; ++p) read_piece(fr[0], sm, 0, p);
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    int kt = 0;
+    for (; kt + QNSTAGE - 1 < KT; ++kt) slice(kt, yes{}, yes{});
+    for (; kt + 1 < KT; ++kt) slice(kt, no{}, yes{});
+    slice(kt, no{}, no{});
+
+    // epilogue: element e of acc[mt][nt] is row 8(e/4) + 4 frag_half + e%4 of
+    // the 32x32 tile, column frag_row.  The per-column and per-row factors
+    // are loaded once (the pointers are uniform), then per element the
+    // scalar path's arithmetic: fp32 scale product, one multiply, one add.
+    float cs[4], bv[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const int n = n0 + wn * 128 + nt * 32 + frag_row;
+        cs[nt] = col_scale ? col_scale[n] : scale_b;
+        bv[nt] = bias ? bias[n] : 0.0f;
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        float rs[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int m = m0 + wm * 128 + mt * 32 + 8 * (e >> 2) + 4 * frag_half + (e & 3);
+            rs[e] = row_scale ? row_scale[m] : scale_a;
+        }
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const int n = n0 + wn * 128 + nt * 32 + frag_row;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm * 128 + mt * 32 + 8 * (e >> 2) + 4 * frag_half + (e & 3);
+                float c = (float)acc[mt][nt][e] * (rs[e] * cs[nt]);
+                if (bias) c = c + bv[nt];
+                C[(int64_t)m * N + n] = c;
+            }
+        }
+    }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -265,6 +530,12 @@ hipError_t launch_int8(const int8_t* A, const int8_t* B, float* C, int M, int N,
         const hipError_t e = stream_workspace(int8_decode_workspace_size(M, N, K), s, &ws);
         if (e != hipSuccess) return e;
         return launch_int8_decode(A, B, C, M, N, K, scale_a, scale_b, row_scale, col_scale, bias, ws, s);
+    }
+    if (vec && M % QBM == 0 && N % QBN == 0 && K % QBK == 0) {
+        const int nt = (M / QBM) * (N / QBN);
+        hipLaunchKernelGGL(int8_dma_kernel, dim3(nt), dim3(256), 0, s, A, B, C, M, N, K, scale_a,
+                           scale_b, row_scale, col_scale, bias);
+        return hipGetLastError();
     }
     if (vec) {
         const int nt = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);

@@ -173,11 +173,14 @@ def test_registry_path(dev):
 
 # ---- matmulInt8 ---------------------------------------------------------------
 # Paths: rows not 16-byte aligned (K or N % 16 != 0) take the SIMT kernel;
-# M <= 16 the streaming split-K kernel with integer atomics; larger M the
-# 32x32x32 MFMA tiles (ragged M/N edges, K tails of a 64-row slice).
+# M <= 16 the streaming split-K kernel; M, N multiples of 256 and K of 64 the
+# LDS-DMA ring (1, 2, 3 and 32 slices); other larger M the 128x128 MFMA tiles
+# (ragged M/N edges, K tails of a 64-row slice).
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (8, 33, 70), (64, 64, 64), (130, 200, 515),
                                    (1, 256, 64), (5, 48, 16), (8, 8192, 8192), (16, 4096, 1040),
-                                   (17, 144, 80), (200, 272, 144), (512, 768, 1024)])
+                                   (17, 144, 80), (200, 272, 144), (512, 768, 1024),
+                                   (256, 256, 64), (256, 512, 128), (512, 256, 192),
+                                   (1024, 1024, 2048)])
 def test_int8_bit_exact(dev, M, N, K):
     case(f"matmulInt8 {M}x{N}x{K}")
     A = I.int8_uniform(1, 0, (M, K))
@@ -250,7 +253,8 @@ def _fill(d, t):
 
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (8, 8192, 1024), (37, 129, 300), (256, 96, 4096)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (8, 8192, 1024), (37, 129, 300), (256, 96, 4096),
+                                   (256, 512, 2048)])
 def test_w8a8_bit_exact(dev, M, N, K):
     """Per-token / per-channel W8A8 (jules_hip_matmul_w8a8) against the numpy
     restatement, bit for bit, with and without bias and per-token scales."""
