@@ -118,7 +118,9 @@ int jules_hip_activation(int act, float* out, const float* in, int64_t n,
  * which are non-causal with scale fixed at 1/sqrtf(D) (:135); causal = 1
  * excludes keys j > query i.
  * dtype JH_F32 or JH_BF16 (Q, K, V, O share it); softmax statistics are fp32.
- * D must be 64 or 128.  S >= 1.  scale must be finite and > 0.
+ * 1 <= D <= 128 (the kernels are built for 64 and 128; other head dims are
+ * zero-padded to the next of the two in a library-held per-stream buffer).
+ * S >= 1.  scale must be finite and > 0.
  * lse (optional, fp32 [B,H,S]) receives the natural-log log-sum-exp of the
  * scaled, masked scores of each row.
  */
@@ -135,7 +137,8 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale,
  * (FlashAttention.h:130-309); this is the training path for the forward above.
  * dtype JH_BF16 (JH_F32 returns JH_ERR_UNSUPPORTED); Q, K, V, O, dO, dQ, dK,
  * dV [B,H,S,D] of that dtype, 16-byte aligned; lse fp32 [B,H,S] as written by
- * the forward with the same causal and scale; D 64 or 128.  fp32
+ * the forward with the same causal and scale; 1 <= D <= 128 (padded as in
+ * the forward).  fp32
  * accumulation; deterministic (no atomics).
  * workspace: jules_hip_flash_attn_bwd_workspace_size(B,H,S) bytes (fp32
  * dvec), 4-byte aligned, no initialisation.

@@ -124,7 +124,8 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale, const void* Q, 
                              void* stream) {
     if (dtype != JH_F32 && dtype != JH_BF16) return fail(JH_ERR_DTYPE, "flash: dtype %d", dtype);
     if (B < 0 || H < 0 || S < 0) return fail(JH_ERR_SHAPE, "flash: B=%d H=%d S=%d", B, H, S);
-    if (D != 64 && D != 128) return fail(JH_ERR_UNSUPPORTED, "flash: head_dim %d (64 or 128)", D);
+    if (D < 1) return fail(JH_ERR_SHAPE, "flash: head_dim %d", D);
+    if (D > 128) return fail(JH_ERR_UNSUPPORTED, "flash: head_dim %d (at most 128)", D);
     if (!(std::isfinite(scale) && scale > 0.0f)) return fail(JH_ERR_ARG, "flash: scale %g", scale);
     if (causal != 0 && causal != 1) return fail(JH_ERR_ARG, "flash: causal must be 0 or 1");
     if ((int64_t)B * H * S * D > kMaxElems) return fail(JH_ERR_SHAPE, "flash: too large");
@@ -133,6 +134,10 @@ int jules_hip_flash_attn_fwd(int dtype, int causal, float scale, const void* Q, 
     if (!aligned(Q, 16) || !aligned(K, 16) || !aligned(V, 16) || !aligned(O, 16) ||
         !aligned(lse, 4))
         return fail(JH_ERR_ALIGN, "flash: Q, K, V, O must be 16-byte aligned");
+    if (D != 64 && D != 128)
+        return check_hip(jh::launch_flash_fwd_padded(dtype, causal, scale, Q, K, V, O, lse, B, H, S, D,
+                                                     static_cast<hipStream_t>(stream)),
+                         "flash launch (padded head dim)");
     return check_hip(jh::launch_flash_fwd(dtype, causal, scale, Q, K, V, O, lse, B, H, S, D,
                                           static_cast<hipStream_t>(stream)),
                      "flash launch");
@@ -149,7 +154,8 @@ int jules_hip_flash_attn_bwd(int dtype, int causal, float scale, const void* Q, 
                              void* workspace, size_t workspace_bytes, void* stream) {
     if (dtype != JH_F32 && dtype != JH_BF16) return fail(JH_ERR_DTYPE, "flash bwd: dtype %d", dtype);
     if (B < 0 || H < 0 || S < 0) return fail(JH_ERR_SHAPE, "flash bwd: B=%d H=%d S=%d", B, H, S);
-    if (D != 64 && D != 128) return fail(JH_ERR_UNSUPPORTED, "flash bwd: head_dim %d (64 or 128)", D);
+    if (D < 1) return fail(JH_ERR_SHAPE, "flash bwd: head_dim %d", D);
+    if (D > 128) return fail(JH_ERR_UNSUPPORTED, "flash bwd: head_dim %d (at most 128)", D);
     if (dtype != JH_BF16) return fail(JH_ERR_UNSUPPORTED, "flash bwd: only bf16 is implemented");
     if (!(std::isfinite(scale) && scale > 0.0f)) return fail(JH_ERR_ARG, "flash bwd: scale %g", scale);
     if (causal != 0 && causal != 1) return fail(JH_ERR_ARG, "flash bwd: causal must be 0 or 1");
@@ -165,6 +171,11 @@ int jules_hip_flash_attn_bwd(int dtype, int causal, float scale, const void* Q, 
     if (!workspace || workspace_bytes < need)
         return fail(JH_ERR_WORKSPACE, "flash bwd: workspace %zu bytes, need %zu", workspace_bytes, need);
     if (!aligned(workspace, 4)) return fail(JH_ERR_ALIGN, "flash bwd: workspace alignment");
+    if (D != 64 && D != 128)
+        return check_hip(jh::launch_flash_bwd_padded(dtype, causal, scale, Q, K, V, O, dO, lse, dQ, dK,
+                                                     dV, B, H, S, D, workspace,
+                                                     static_cast<hipStream_t>(stream)),
+                         "flash bwd launch (padded head dim)");
     return check_hip(jh::launch_flash_bwd(dtype, causal, scale, Q, K, V, O, dO, lse, dQ, dK, dV, B,
                                           H, S, D, workspace, static_cast<hipStream_t>(stream)),
                      "flash bwd launch");

@@ -77,4 +77,19 @@ hipError_t launch_pj_reduce(const float* in, float* out, int64_t n_out, int64_t 
 // calibration: workgroups x 4 waves x 16*iters MFMAs on random operands
 hipError_t launch_mfma_ceiling(float* out, int workgroups, int iters, hipStream_t s);
 
+
+// flash attention at head dims other than 64 and 128 (1 <= D <= 128): inputs
+// zero-padded to 64 or 128 in the per-stream workspace (flash_pad.hip)
+int flash_padded_dim(int D);
+hipError_t launch_flash_fwd_padded(int dtype, int causal, float scale, const void* Q, const void* K,
+                                   const void* V, void* O, float* lse, int B, int H, int S, int D,
+                                   hipStream_t s);
+hipError_t launch_flash_bwd_padded(int dtype, int causal, float scale, const void* Q, const void* K,
+                                   const void* V, const void* O, const void* dO, const float* lse,
+                                   void* dQ, void* dK, void* dV, int B, int H, int S, int D,
+                                   void* bwd_ws, hipStream_t s);
+// device memory of `need` bytes for entry points without a workspace
+// argument: one buffer per (device, stream), kept for the process
+hipError_t stream_workspace(size_t need, hipStream_t s, void** ws);
+
 }  // namespace jh

@@ -30,9 +30,6 @@
 // design instead (int8_dma_kernel below).  Shapes whose rows are not 16-byte
 // aligned (K or N not a multiple of 16, or misaligned pointers) take a plain
 // LDS-tiled SIMT kernel.
-#include <map>
-#include <mutex>
-
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -493,32 +490,6 @@ __global__ __launch_bounds__(256, 1) void int8_dma_kernel(
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
-
-// Workspace of the decode path, one per (device, stream) and kept for the
-// process: calls on one stream run in order and may share it, calls on other
-// streams get their own.  A larger need replaces it once the stream has
-// finished with the old one.
-hipError_t stream_workspace(size_t need, hipStream_t s, void** ws) {
-    static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> cache;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lock(mu);
-    auto& slot = cache[{dev, s}];
-    if (slot.second < need) {
-        if (slot.first) {
-            if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
-            (void)hipFree(slot.first);
-        }
-        slot = {nullptr, 0};
-        void* p = nullptr;
-        if ((e = hipMalloc(&p, need)) != hipSuccess) return e;
-        slot = {p, need};
-    }
-    *ws = slot.first;
-    return hipSuccess;
-}
 
 hipError_t launch_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                        float scale_a, float scale_b, const float* row_scale, const float* col_scale,

@@ -105,7 +105,8 @@ def test_gemm_validation(args, status):
 
 @pytest.mark.parametrize("args,status", [
     ((7, 0, 0.125, P, P, P, P, None, 1, 1, 8, 64, None), DTYPE),
-    ((0, 0, 0.125, P, P, P, P, None, 1, 1, 8, 96, None), UNSUP),
+    ((0, 0, 0.125, P, P, P, P, None, 1, 1, 8, 160, None), UNSUP),   # head_dim > 128
+    ((0, 0, 0.125, P, P, P, P, None, 1, 1, 8, 0, None), SHAPE),
     ((0, 0, float("nan"), P, P, P, P, None, 1, 1, 8, 64, None), ARG),
     ((0, 0, -1.0, P, P, P, P, None, 1, 1, 8, 64, None), ARG),
     ((0, 2, 0.125, P, P, P, P, None, 1, 1, 8, 64, None), ARG),

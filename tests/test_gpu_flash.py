@@ -2,7 +2,9 @@
 
 Bars (normwise, against the fp64 oracle): 1e-5 for fp32, 1e-2 for bf16.
 Full-size configs are checked on sampled heads/rows against the fp64 oracle
-and on every head against a torch fp32 evaluation on the GPU."""
+and on every head against a torch fp32 evaluation on the GPU.  Head dims
+other than 64 and 128 (zero-padded to the next of the two) are checked at
+the same bars."""
 import numpy as np
 import pytest
 import torch
@@ -24,7 +26,11 @@ def _run(dev, Q, K, V, dt, causal, scale=None, lse=None):
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("B,H,S,D", [(1, 1, 1, 64), (1, 2, 37, 64), (2, 1, 128, 128),
-                                     (1, 3, 200, 128), (1, 1, 129, 64), (2, 2, 300, 64)])
+                                     (1, 3, 200, 128), (1, 1, 129, 64), (2, 2, 300, 64),
+                                     # head dims zero-padded to 64 / 128
+                                     (1, 2, 70, 8), (2, 1, 100, 32), (1, 2, 130, 48),
+                                     (1, 1, 257, 80), (2, 2, 96, 96), (1, 2, 65, 100),
+                                     (1, 1, 64, 127)])
 def test_small_against_fp64(dev, dt, causal, B, H, S, D):
     case(f"flash {dt} causal={causal} [{B},{H},{S},{D}]")
     Q, K, V = I.attn_inputs(B, H, S, D, dt, seed=S + D)

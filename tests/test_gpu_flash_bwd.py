@@ -34,7 +34,10 @@ def _inputs(B, H, S, D, seed):
 
 
 @pytest.mark.parametrize("B,H,S,D", [(1, 1, 1, 64), (1, 2, 37, 64), (2, 2, 128, 128),
-                                     (1, 3, 200, 128), (2, 4, 256, 64), (1, 2, 333, 128)])
+                                     (1, 3, 200, 128), (2, 4, 256, 64), (1, 2, 333, 128),
+                                     # head dims zero-padded to 64 / 128
+                                     (1, 2, 70, 32), (2, 1, 100, 96), (1, 1, 129, 80),
+                                     (1, 2, 37, 100)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_against_fp64(dev, B, H, S, D, causal):
     case(f"flash bwd B{B} H{H} S{S} D{D} causal={causal}")
@@ -78,14 +81,19 @@ def test_deterministic(dev):
 def test_validation(dev):
     L = _lib.lib()
     f = L.jules_hip_flash_attn_bwd
-    P = 0x10000
+    P = 0x10000  # placeholder device address: every case below must fail validation
     args = [1, 1, 0.125] + [P] * 9 + [1, 1, 16, 128, P, 1 << 20, None]
     bad = list(args)
     bad[0] = 0  # fp32: not implemented
     assert f(*bad) == 8
+    # head dims beyond 128 are rejected before any launch (every D up to 128
+    # is supported, so a smaller one would launch on the placeholder pointers)
     bad = list(args)
-    bad[15] = 96  # head dim
+    bad[15] = 160
     assert f(*bad) == 8
+    bad = list(args)
+    bad[15] = 0
+    assert f(*bad) == 2
     bad = list(args)
     bad[17] = 0  # workspace bytes
     assert f(*bad) == 6
