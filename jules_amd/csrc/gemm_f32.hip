@@ -109,68 +109,85 @@ __global__ __launch_bounds__((BM / TM) * (BN / TN)) void gemm_f32_kernel(
 }
 
 // Small problems (C1: 512^3): one wave per SIMD is all the outputs give at
-// 2x2 per thread, and then the LDS reads (four values per four fmas, at most
-// one read per ~30 cycles per wave) set the pace.  This kernel reads no LDS:
-// a wave owns R rows x 64 columns, lane = column.  Per k it loads B[k][n0 +
-// lane] (one coalesced 256-byte row segment) and takes A[m][k] from SGPRs
-// (wave-uniform scalar loads), then issues R independent fmas.  Every output
-// is still one fma chain over k = 0..K-1 in order.  At 512^3 it takes
-// 29.7 us against 32.6 us for the 32x32 LDS-tiled kernel; B-load latency
-// bounds it (eight loads in flight per wave: deeper rings make the compiler
-// hoist more A scalar loads than the SGPR file holds).
+// 2x2 per thread, and then the LDS reads of both operands (four values per
+// four fmas, at most one read per ~30 cycles per wave) set the pace.  Here a
+// wave owns RW rows x 64 columns, lane = column.  The workgroup's RW*RWV rows
+// of A are staged in LDS once (K <= ROWS_MAX_K) and read back as broadcasts
+// (every lane the same address, one ds_read_b128 per row per four k).  B is
+// streamed from global memory: per k one coalesced 256-byte row segment, a
+// ring of PB groups of KU rows in flight per wave.  Every output is still one
+// fma chain over k = 0..K-1 in order.  At 512^3: 21.7 us (the 32x32 LDS-tiled
+// kernel 32.6 us); 1 or 4 rows per wave measured 27.1 and 26.8 us.
 constexpr int RW = 2;    // rows per wave
 constexpr int RWV = 4;   // waves per workgroup (4 x RW rows x 64 columns)
-constexpr int KU = 4;    // k unroll
+constexpr int KU = 4;    // k per group (one ds_read_b128 of A per row)
+constexpr int ROWS_MAX_K = 2048;  // RW * RWV rows of K floats in LDS: 64 KiB
 
 template <int ACT>
 __global__ __launch_bounds__(64 * RWV) void gemm_f32_rows_kernel(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ bias,
     float* __restrict__ C, int M, int N, int K) {
+    extern __shared__ float sA[];  // [RW * RWV][Kp]
+    const int Kp = (K + 3) & ~3;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = blockIdx.x * 64 + lane;
     const int nc = min(n, N - 1);  // columns past N compute on a valid column, never stored
-    const int m0 = (blockIdx.y * RWV + wave) * RW;
+    const int mb = blockIdx.y * RW * RWV;
+    // stage rows mb .. mb + RW*RWV - 1 of A (rows past M repeat row M-1)
+    for (int i = threadIdx.x; i < RW * RWV * K; i += 64 * RWV) {
+        const int r = i / K, k = i - r * K;
+        sA[r * Kp + k] = A[(int64_t)min(mb + r, M - 1) * K + k];
+    }
+    __syncthreads();
     const float* arow[RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) arow[r] = A + (int64_t)min(m0 + r, M - 1) * K;
+    for (int r = 0; r < RW; ++r) arow[r] = sA + (wave * RW + r) * Kp;
     const float* bcol = B + nc;
 
     float acc[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
     // Groups of KU k-steps.  The B row segments of group g+PB are loaded while
-    // group g is computed (a ring of PB groups in registers); A comes through
-    // wave-uniform scalar loads.
-    constexpr int PB = 2;
+    // group g is computed (a ring of PB groups in registers).  Prefetches past
+    // the last group reload the last group (never used), so every load is
+    // unconditional.
+    constexpr int PB = 8;
     const int ng = K / KU;
+    const int64_t nstride = N;
     float bq[PB][KU];
     auto load_b = [&](float(&dst)[KU], int g) {
+        const float* p = bcol + (int64_t)min(g, ng - 1) * KU * nstride;
 #pragma unroll
-        for (int u = 0; u < KU; ++u) dst[u] = bcol[(int64_t)(g * KU + u) * N];
+        for (int u = 0; u < KU; ++u) dst[u] = p[u * nstride];
     };
-    auto fma_group = [&](const float(&b)[KU], int g) {
+    // group g: B in ring slot i
+    auto step = [&](int i, int g) {
+        float4 a[RW];
 #pragma unroll
-        for (int u = 0; u < KU; ++u)
+        for (int r = 0; r < RW; ++r) a[r] = *reinterpret_cast<const float4*>(arow[r] + g * KU);
 #pragma unroll
-            for (int r = 0; r < RW; ++r) acc[r] = __builtin_fmaf(arow[r][g * KU + u], b[u], acc[r]);
-    };
-#pragma unroll
-    for (int i = 0; i < PB; ++i)
-        if (i < ng) load_b(bq[i], i);
-    int g = 0;
-    for (; g + PB <= ng; g += PB) {
-#pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            fma_group(bq[i], g + i);
-            if (g + i + PB < ng) load_b(bq[i], g + i + PB);
+        for (int r = 0; r < RW; ++r) {
+            acc[r] = __builtin_fmaf(a[r].x, bq[i][0], acc[r]);
+            acc[r] = __builtin_fmaf(a[r].y, bq[i][1], acc[r]);
+            acc[r] = __builtin_fmaf(a[r].z, bq[i][2], acc[r]);
+            acc[r] = __builtin_fmaf(a[r].w, bq[i][3], acc[r]);
         }
-    }
-    // the last ng % PB groups (their B is in ring slots 0..); ng % PB < PB, so
-    // group g + i sits in slot i (g is a multiple of PB)
+        load_b(bq[i], g + PB);
+    };
+    int g = 0;
+    if (ng > 0) {
 #pragma unroll
-    for (int i = 0; i < PB - 1; ++i)
-        if (g + i < ng) fma_group(bq[i], g + i);
+        for (int i = 0; i < PB; ++i) load_b(bq[i], i);
+        for (; g + PB <= ng; g += PB) {
+#pragma unroll
+            for (int i = 0; i < PB; ++i) step(i, g + i);
+        }
+        // the last ng % PB groups: group g + i sits in ring slot i (g is a multiple of PB)
+#pragma unroll
+        for (int i = 0; i < PB - 1; ++i)
+            if (g + i < ng) step(i, g + i);
+    }
     for (int k = ng * KU; k < K; ++k) {
         const float b = bcol[(int64_t)k * N];
 #pragma unroll
@@ -180,7 +197,7 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rows_kernel(
     const float bv = bias ? bias[n] : 0.0f;
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-        const int m = m0 + r;
+        const int m = mb + wave * RW + r;
         if (m >= M) continue;
         float v = acc[r];
         if (bias) v = v + bv;
@@ -214,12 +231,13 @@ hipError_t launch_gemm_f32(int act, const float* A, const float* B, const float*
     // as 512^3, which then still launches 256 workgroups.
     const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
     hipError_t e = hipSuccess;
-    if ((int64_t)M * N <= (1 << 20)) {
-        // up to 1M outputs: the LDS-free row-wave kernel (4096 waves at most)
+    if ((int64_t)M * N <= (1 << 20) && K <= ROWS_MAX_K) {
+        // up to 1M outputs: the row-wave kernel (8192 waves at most)
         dim3 grid((N + 63) / 64, (M + RW * RWV - 1) / (RW * RWV));
+        const size_t lds = (size_t)RW * RWV * ((K + 3) & ~3) * sizeof(float);
         JH_DISPATCH_ACT(act, ACT, {
-            hipLaunchKernelGGL(gemm_f32_rows_kernel<ACT>, grid, dim3(64 * RWV), 0, s, A, B, bias, C, M,
-                               N, K);
+            hipLaunchKernelGGL(gemm_f32_rows_kernel<ACT>, grid, dim3(64 * RWV), lds, s, A, B, bias, C,
+                               M, N, K);
             e = hipGetLastError();
         });
     } else if (tiles64 >= 512) {
