@@ -8,7 +8,8 @@ synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 (2*M*N*K + 4*B*H*D*S*(S+1)/2 FLOP per step) over the timed steps.
 
 The same run also times every BASELINE config on its own (per_config, keys
-c1-c5), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
+c1-c5), the reference's published fp32 GEMM shape (per_config, key g1,
+beside its published time), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
 entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
 (per_config, keys m1-m2, fp32 TFLOP/s), the flash-attention backward at C4's
 shape (per_config, key b4), matmulInt8 (per_config, keys i1-i2: int8 TOP/s at
@@ -77,6 +78,15 @@ ROW_CONFIGS = {
 }
 
 
+# The reference's published fp32 GEMM shape (benchmarks/bench_comparison.py:
+# 141-145): [64,784] x [784,256], no bias or activation, 0.090 ms on four
+# AVX-512 cores with MKL.  Not a BASELINE config; the row-wave fp32 kernel.
+GEMM_CONFIGS = {
+    "g1": dict(kind="gemm", dtype="f32", M=64, N=256, K=784, act="none", bias=False,
+               reference_published_ms=0.090),
+}
+
+
 # The 2-layer MLP forward + loss + backward (interleavedMLPForwardBackward):
 # the reference benchmark's shape (bench_kernel.cpp:268-271, launch-latency
 # bound on a GPU) and a large one where the fp32 MFMA GEMMs dominate.
@@ -136,6 +146,8 @@ class Runner:
                 self.A = torch.rand((M, K), generator=g, device=dev) * 2 - 1
                 self.B = torch.rand((K, N), generator=g, device=dev) * 2 - 1
                 self.bias = torch.rand((N,), generator=g, device=dev) * 2 - 1
+                if not s.get("bias", True):
+                    self.bias = None
                 self.C = torch.empty((M, N), device=dev)
             else:
                 std = K ** -0.5
@@ -425,7 +437,7 @@ def main():
 
     # ---- per-config launch timings -----------------------------------------
     per = {}
-    ALL = {**CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS, **INT8_CONFIGS}
+    ALL = {**CONFIGS, **GEMM_CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS, **INT8_CONFIGS}
     names = [n for n in ALL if not args.only or n in args.only.split(",")]
     if args.step_only:
         names = []
