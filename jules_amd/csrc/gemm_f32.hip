@@ -118,12 +118,11 @@ __global__ __launch_bounds__((BM / TM) * (BN / TN)) void gemm_f32_kernel(
 // ring of PB groups of KU rows in flight per wave.  Every output is still one
 // fma chain over k = 0..K-1 in order.  At 512^3: 21.7 us (the 32x32 LDS-tiled
 // kernel 32.6 us); 1 or 4 rows per wave measured 27.1 and 26.8 us.
-constexpr int RW = 2;    // rows per wave
 constexpr int RWV = 4;   // waves per workgroup (4 x RW rows x 64 columns)
 constexpr int KU = 4;    // k per group (one ds_read_b128 of A per row)
-constexpr int ROWS_MAX_K = 2048;  // RW * RWV rows of K floats in LDS: 64 KiB
+constexpr int ROWS_MAX_K = 2048;  // RW * RWV rows of K floats in LDS: 64 KiB at RW = 2
 
-template <int ACT>
+template <int ACT, int RW>  // RW rows per wave
 __global__ __launch_bounds__(64 * RWV) void gemm_f32_rows_kernel(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ bias,
     float* __restrict__ C, int M, int N, int K) {
@@ -232,13 +231,18 @@ hipError_t launch_gemm_f32(int act, const float* A, const float* B, const float*
     const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
     hipError_t e = hipSuccess;
     if ((int64_t)M * N <= (1 << 20) && K <= ROWS_MAX_K) {
-        // up to 1M outputs: the row-wave kernel (8192 waves at most)
-        dim3 grid((N + 63) / 64, (M + RW * RWV - 1) / (RW * RWV));
-        const size_t lds = (size_t)RW * RWV * ((K + 3) & ~3) * sizeof(float);
+        // up to 1M outputs: the row-wave kernel, 2 rows per wave (8192 waves at
+        // most), or 1 row per wave when 2 would leave fewer than 1024 waves
+        // (at 512^3: 21.7 us at 2 rows, 27.1 us at 1 row)
+        const bool one = (int64_t)((N + 63) / 64) * ((M + 1) / 2) < 1024;
+        auto launch = [&](auto kern, int rw) {
+            dim3 grid((N + 63) / 64, (M + rw * RWV - 1) / (rw * RWV));
+            const size_t lds = (size_t)rw * RWV * ((K + 3) & ~3) * sizeof(float);
+            hipLaunchKernelGGL(kern, grid, dim3(64 * RWV), lds, s, A, B, bias, C, M, N, K);
+            return hipGetLastError();
+        };
         JH_DISPATCH_ACT(act, ACT, {
-            hipLaunchKernelGGL(gemm_f32_rows_kernel<ACT>, grid, dim3(64 * RWV), lds, s, A, B, bias, C,
-                               M, N, K);
-            e = hipGetLastError();
+            e = one ? launch(gemm_f32_rows_kernel<ACT, 1>, 1) : launch(gemm_f32_rows_kernel<ACT, 2>, 2);
         });
     } else if (tiles64 >= 512) {
         JH_DISPATCH_ACT(act, ACT, e = (run<64, 64, 32, 4, 4, ACT>(A, B, bias, C, M, N, K, s)));
