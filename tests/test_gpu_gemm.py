@@ -40,8 +40,9 @@ def test_f32_c1_bit_exact(dev, act):
 
 @pytest.mark.parametrize("M,N,K", [(1, 16, 1), (17, 32, 5), (65, 144, 257), (128, 96, 1000),
                                    (300, 640, 64), (2048, 2048, 96),
-                                   # row-wave kernel at its K limit, and one past it (LDS-tiled)
-                                   (9, 144, 2048), (33, 64, 2100)])
+                                   # row-wave kernel at its K limit (1 and 2 rows per wave: 32
+                                   # and 64 KiB of LDS), and one past it (LDS-tiled)
+                                   (9, 144, 2048), (256, 512, 2048), (33, 64, 2100)])
 def test_f32_shapes_bit_exact(dev, M, N, K):
     case(f"gemm f32 {M}x{N}x{K}")
     A, B, bias = I.gemm_inputs(M, N, K, "f32", seed=M + N + K)
