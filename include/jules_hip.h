@@ -102,10 +102,46 @@ int jules_hip_gemm_bias_act(int dtype, int act, const void* A, const void* B,
                             const float* bias, void* C, int M, int N, int K,
                             void* stream);
 
+/* ---- GEMM tile table -------------------------------------------------------
+ * out[4] = {kernel variant, tile_m, tile_n, tile_k} that
+ * jules_hip_gemm_bias_act launches for this dtype and shape (needs no GPU).
+ * Variants: 0/1 fp32 row kernel with 1/2 rows per wave (tile 4 or 8 rows x
+ * 64 columns, all of K in LDS, K <= 2048), 2/3 fp32 32x32 / 64x64 tiles with
+ * 32-deep K slices, 4 bf16 256x256 tiles with 32-deep LDS-DMA stages, 5 bf16
+ * 256x256 register-staged tiles with 64-deep slices.  Replaces the role of
+ * TilePlanner::getTileConfig (reference TilePlanner.h:74-136), which sizes
+ * tiles for the CPU caches; jules::kernel::TilePlanner returns these.
+ */
+int jules_hip_gemm_tile(int dtype, int M, int N, int K, int* out);
+
+/* ---- general fp32 GEMM (BLAS sgemm) -----------------------------------------
+ * C = alpha * op(A) op(B) + beta * C, row-major, op(X) = X^T when transX = 1;
+ * A is [M,K] (transA = 0) or [K,M] (transA = 1) with row stride lda, B is
+ * [K,N] or [N,K] with row stride ldb, C [M,N] with row stride ldc; lda, ldb,
+ * ldc at least the stored row length (and 1).  beta = 0 writes C without
+ * reading it; K = 0 or alpha = 0 gives beta * C without reading A or B.
+ * Replaces blasMatmul(A,B,C,M,N,K,alpha,beta,transA,transB) (reference
+ * FusedKernels.h:633-644) and the cblas_sgemm calls of the reference
+ * (LLVMBackend.cpp:1242-1255, PJRT.cpp:692-697), which libjules_cblas.so
+ * (include/jules_cblas.h) maps here.
+ * The dense, untransposed alpha = 1, beta = 0 product (what LLVMBackend
+ * emits) runs the fp32 fma-chain GEMM of jules_hip_gemm_bias_act, so its bits
+ * equal the reference's tiledMatmulWithActivation; every other case runs an
+ * fp32 MFMA GEMM (fp32 accumulation in another order; within fp32 rounding
+ * of the exact product, as the reference's BLAS is).  Skinny products split
+ * K through a library-held per-(device, stream) buffer.
+ */
+int jules_hip_sgemm(int transA, int transB, int M, int N, int K, float alpha,
+                    const float* A, int lda, const float* B, int ldb,
+                    float beta, float* C, int ldc, void* stream);
+
 /* ---- elementwise activation ----------------------------------------------
  * out[i] = act(in[i]), fp32, n elements.  act = GELU replaces
  * fusedGelu(out,in,N) (reference FusedKernels.h:606) and the routed name
- * "fusedGelu" (KernelRoutingPass.cpp:287).  In-place (out == in) is allowed.
+ * "fusedGelu" (KernelRoutingPass.cpp:287): elements below n & ~15 get the
+ * vector-path gelu (bit-exact with the reference), the last n % 16 the
+ * reference's scalar tail formula with tanhf (the device libm's tanhf, so
+ * within a few ulp of the reference's).  In-place (out == in) is allowed.
  */
 int jules_hip_activation(int act, float* out, const float* in, int64_t n,
                          void* stream);
@@ -185,7 +221,8 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W,
  * int32 accumulation, B indexed B[k*N+j]; the product scale_A*scale_B is
  * rounded to fp32 first, then one multiply, then one add of bias.
  * (The reference's AVX-512F and VNNI paths index the wrong columns; this
- * entry point follows the scalar path.)  K <= 131072 keeps int32 exact.
+ * entry point follows the scalar path.)  K <= 131071 keeps the int32 sum
+ * exact (every product is at most 2^14); larger K returns JH_ERR_SHAPE.
  */
 int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M,
                           int N, int K, float scale_A, float scale_B,
@@ -200,7 +237,7 @@ int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M,
  * sA_i * sB_j rounded to fp32 per element, one multiply, one add of bias.
  * With constant scale vectors the result equals jules_hip_matmul_int8 bit for
  * bit.  scale_A: fp32 [M] per-token scales, or NULL for 1; scale_B: fp32 [N]
- * per-output-channel scales (required).  K <= 131072.
+ * per-output-channel scales (required).  K <= 131071.
  */
 int jules_hip_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M,
                           int N, int K, const float* scale_A,
@@ -319,8 +356,10 @@ int jules_hip_mfma_ceiling(float* out, int workgroups, int iters, void* stream);
  * fusedSoftmax, (x, gamma, beta) -> y with backend_config "epsilon=<f>"
  * (default 1e-5) for fusedLayerNorm, (logits, targets) -> (grad, loss) for
  * fusedCrossEntropyLoss (loss: one fp32 element); rows are the last
- * dimension.  W8A16 and cross entropy need a workspace; their registry
- * entries allocate one per device on first use.
+ * dimension.  W8A16, cross entropy and the MLP entries need a workspace;
+ * the registry uses a library-held buffer per (device, stream), grown on
+ * demand: calls on one stream share it in stream order, calls on different
+ * streams never share one.
  */
 typedef struct jh_tensor {
     void* data;

@@ -15,6 +15,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "jules_hip.h"
 
@@ -24,9 +25,11 @@ namespace kernel {
 // reference FusedKernels.h:61-67; Silu appended (value 5, C ABI JH_ACT_SILU)
 enum class ActivationType { None, Relu, Sigmoid, Tanh, Gelu, Silu };
 
-// reference TilePlanner.h:39-56.  The GPU kernels pick their own tiles; a
-// TileConfig passed in is accepted and does not change results (the
-// reference's results do not depend on it either).
+// reference TilePlanner.h:39-56.  On the GPU a TileConfig names one kernel of
+// the library's gfx950 tile table (jules_hip_gemm_tile): fp32 rows x 64 x K
+// with 4 or 8 rows (the row kernel), 32x32x32 or 64x64x32.  Every table tile
+// gives the same bits (each output is one fma chain over k in order), as in
+// the reference, whose results do not depend on the tile either.
 struct TileConfig {
     int tile_m;
     int tile_n;
@@ -46,7 +49,13 @@ struct CacheInfo {
     static CacheInfo detect();
 };
 
-// reference TilePlanner.h:74-295: a static gfx950 tile table, no timing.
+// reference TilePlanner.h:74-294.  computeAnalytical returns the tile the
+// fp32 GEMM launch uses by default (the library's table); getTileConfig
+// caches per shape and, with auto-tuning on (the default, as in the
+// reference) and M, N >= 32, times every table kernel that can run the
+// shape on the current GPU (one warm-up and 10 timed launches each, HIP
+// events) and keeps the fastest.  Like the reference, one planner object is
+// not safe to use from two threads at once.
 class TilePlanner {
 public:
     explicit TilePlanner(const CacheInfo& cache = CacheInfo::detect());
@@ -57,9 +66,15 @@ public:
     const CacheInfo& cacheInfo() const { return cache_; }
 
 private:
+    TileConfig autoTune(int M, int N, int K, const TileConfig& defaultConfig);
+    struct Entry {
+        int m, n, k;
+        TileConfig cfg;
+    };
     CacheInfo cache_;
     bool autoTune_ = true;
     bool verbose_ = false;
+    std::vector<Entry> configCache_;
 };
 
 // reference ExecutionArena.h:94-199: bump allocator over one DEVICE buffer
@@ -99,9 +114,16 @@ void fusedMatmulRelu(const float* X, const float* W, float* output, int M, int K
 // reference FusedKernels.h:265
 void fusedMatmulBiasRelu(const float* X, const float* W, const float* bias, float* output, int M,
                          int K, int N);
-// reference FusedKernels.h:378
+// reference FusedKernels.h:378.  A cfg naming a kernel of the tile table
+// (what TilePlanner returns) runs that kernel; any other cfg runs the
+// table's default for the shape.  The bits are the same either way.
 void tiledMatmulWithActivation(const float* A, const float* B, float* C, int M, int N, int K,
                                const TileConfig& cfg, ActivationType act = ActivationType::None);
+// reference FusedKernels.h:633-644: C = alpha op(A) op(B) + beta C with the
+// reference's leading dimensions (A [M,K] or [K,M], B [K,N] or [N,K], C
+// [M,N], all dense); jules_hip_sgemm
+void blasMatmul(const float* A, const float* B, float* C, int M, int N, int K, float alpha = 1.0f,
+                float beta = 0.0f, bool transA = false, bool transB = false);
 // reference FusedKernels.h:606
 void fusedGelu(float* output, const float* input, int N);
 // reference FusedKernels.h:464
@@ -151,10 +173,21 @@ void matmulInt8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
 // reference FlashAttention.h:130 (non-causal, scale 1/sqrtf(head_dim))
 void flashAttention(float* output, const float* Q, const float* K, const float* V, int batch,
                     int heads, int seq, int head_dim, ExecutionArena& arena, TilePlanner& planner);
-// reference FlashAttention.h:114
+// reference FusedKernels.h:1085-1115: flash attention when the [S,S] fp32
+// score matrix exceeds l3_bytes, or when seq_len >= 64 and head_dim <= 256
+inline bool shouldUseFlashAttention(int seq_len, int head_dim, size_t l3_bytes) {
+    const size_t attn_matrix_bytes = (size_t)seq_len * seq_len * sizeof(float);
+    if (attn_matrix_bytes > l3_bytes) return true;
+    return seq_len >= 64 && head_dim <= 256;
+}
+// reference FlashAttention.h:114-124: chooses with shouldUseFlashAttention and
+// planner.cacheInfo().l3_bytes between flashAttention and standardAttention
 void attention(float* output, const float* Q, const float* K, const float* V, int batch,
                int heads, int seq, int head_dim, ExecutionArena& arena, TilePlanner& planner);
-// reference FlashAttention.h:52 (same result as flashAttention on the GPU)
+// reference FlashAttention.h:52-100: softmax(Q K^T / sqrt(D)) V, non-causal.
+// On the GPU it runs the flash kernel (the same function; the reference
+// materialises the [S,S] matrix only because that is faster on a CPU for
+// small S), then resets the arena as the reference does.
 void standardAttention(float* output, const float* Q, const float* K, const float* V, int batch,
                        int heads, int seq, int head_dim, ExecutionArena& arena);
 

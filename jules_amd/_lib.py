@@ -37,6 +37,9 @@ SIGNATURES = {
     "jules_hip_status_string": (ctypes.c_char_p, [_int]),
     "jules_hip_last_error": (ctypes.c_char_p, []),
     "jules_hip_gemm_bias_act": (_int, [_int, _int, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "jules_hip_gemm_tile": (_int, [_int, _int, _int, _int, ctypes.POINTER(_int)]),
+    "jules_hip_sgemm": (_int, [_int, _int, _int, _int, _int, _f32, _vp, _int, _vp, _int, _f32, _vp,
+                               _int, _vp]),
     "jules_hip_activation": (_int, [_int, _vp, _vp, _i64, _vp]),
     "jules_hip_flash_attn_fwd": (_int, [_int, _int, _f32, _vp, _vp, _vp, _vp, _vp, _int, _int,
                                         _int, _int, _vp]),

@@ -17,7 +17,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(ROOT, "_build")
 LIB = os.path.join(HERE, "libjules_hip.so")
-HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.environ.get("HIPCC", f"{ROCM}/bin/hipcc")
 ARCH = "gfx950"
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", f"-I{INCLUDE}", f"-I{CSRC}",
@@ -58,13 +59,35 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    _build_cblas(verbose)
     _build_selftests(verbose)
     return LIB
 
 
+CBLAS_LIB = os.path.join(HERE, "libjules_cblas.so")
+
+
+def _build_cblas(verbose):
+    """libjules_cblas.so: the cblas_sgemm symbol (include/jules_cblas.h), a
+    host-only layer over libjules_hip.so, kept in its own library so that
+    loading libjules_hip.so never interposes a BLAS."""
+    tmp = CBLAS_LIB + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-Wall", "-fPIC", "-shared", f"-I{INCLUDE}",
+           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", os.path.join(CSRC, "cblas_sgemm.cpp"),
+           f"-L{HERE}", "-ljules_hip", f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN",
+           f"-Wl,-rpath,{ROCM}/lib", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on cblas_sgemm.cpp:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CBLAS_LIB)
+
+
 def _build_selftests(verbose):
     """Host-only C++ test programs tests/cpp/<name>_selftest.cpp, linked
-    against the library (g++)."""
+    against the library and the HIP runtime (g++; they allocate device
+    buffers to call the library with)."""
     cdir = os.path.join(ROOT, "tests", "cpp")
     if not os.path.isdir(cdir):
         return
@@ -73,13 +96,25 @@ def _build_selftests(verbose):
             continue
         src = os.path.join(cdir, f)
         out = os.path.join(cdir, f[:-4])
-        cmd = ["g++", "-O2", "-std=c++17", f"-I{INCLUDE}", src, f"-L{HERE}", "-ljules_hip",
-               "-Wl,-rpath,$ORIGIN/../../jules_amd", "-o", out]
+        cmd = ["g++", "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", "-D__HIP_PLATFORM_AMD__",
+               f"-I{ROCM}/include", src, f"-L{HERE}", "-ljules_hip", f"-L{ROCM}/lib",
+               "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../jules_amd", f"-Wl,-rpath,{ROCM}/lib",
+               "-o", out]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"g++ failed on {src}:\n{r.stdout}\n{r.stderr}")
+    # a plain C caller that binds cblas_sgemm through dlopen, as a JIT's
+    # process-symbol lookup would (no link-time dependency on the library)
+    src = os.path.join(cdir, "cblas_dlopen.c")
+    if os.path.exists(src):
+        cmd = ["gcc", "-O2", "-std=c11", "-Wall", src, "-ldl", "-lm", "-o", os.path.join(cdir, "cblas_dlopen")]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"gcc failed on {src}:\n{r.stdout}\n{r.stderr}")
 
 
 if __name__ == "__main__":

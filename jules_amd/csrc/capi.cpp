@@ -14,11 +14,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <mutex>
 #include <string>
 
 #include "jules_hip.h"
 #include "launch.hpp"
+#include "tiles.hpp"
 
 namespace {
 
@@ -46,6 +46,10 @@ bool valid_act(int act) { return act >= JH_ACT_NONE && act <= JH_ACT_SILU; }
 // against sizes whose products overflow int64 in the caller's arithmetic.
 constexpr int64_t kMaxElems = int64_t(1) << 40;
 
+// largest int8 GEMM depth whose int32 sums cannot overflow: every product
+// is at most (-128)*(-128) = 2^14, and 131071 * 2^14 < 2^31
+constexpr int kMaxInt8K = 131071;
+
 }  // namespace
 
 namespace jh {
@@ -54,6 +58,26 @@ namespace jh {
 int set_last_error(int status, const std::string& message) {
     g_last_error = message;
     return status;
+}
+
+// jules_hip_gemm_bias_act for fp32 with a chosen kernel of the tile table
+// (variant < 0: the table's default for the shape).  Every variant gives the
+// same bits, so the choice changes speed only.
+int gemm_f32_with_variant(int variant, int act, const float* A, const float* B, const float* bias,
+                          float* C, int M, int N, int K, hipStream_t s) {
+    if (!valid_act(act)) return fail(JH_ERR_ACT, "gemm: activation code %d", act);
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "gemm: M=%d N=%d K=%d", M, N, K);
+    if ((int64_t)M * K > kMaxElems || (int64_t)K * N > kMaxElems || (int64_t)M * N > kMaxElems)
+        return fail(JH_ERR_SHAPE, "gemm: M=%d N=%d K=%d too large", M, N, K);
+    if (variant < 0) variant = f32_gemm_tile(M, N, K).variant;
+    if (!f32_variant_valid(variant, K))
+        return fail(JH_ERR_ARG, "gemm f32: kernel variant %d cannot run K=%d", variant, K);
+    if (M == 0 || N == 0) return JH_OK;
+    if (!C || (K > 0 && (!A || !B))) return fail(JH_ERR_NULL, "gemm: null A, B or C");
+    if (!aligned(A, 4) || !aligned(B, 4) || !aligned(C, 4) || !aligned(bias, 4))
+        return fail(JH_ERR_ALIGN, "gemm f32: operands must be 4-byte aligned");
+    return check_hip(launch_gemm_f32_variant(variant, act, A, B, bias, C, M, N, K, s),
+                     "gemm f32 launch");
 }
 }  // namespace jh
 
@@ -87,17 +111,13 @@ int jules_hip_gemm_bias_act(int dtype, int act, const void* A, const void* B, co
     if ((int64_t)M * K > kMaxElems || (int64_t)K * N > kMaxElems || (int64_t)M * N > kMaxElems)
         return fail(JH_ERR_SHAPE, "gemm: M=%d N=%d K=%d too large", M, N, K);
     if (dtype != JH_F32 && dtype != JH_BF16) return fail(JH_ERR_DTYPE, "gemm: dtype %d", dtype);
+    if (dtype == JH_F32)
+        return jh::gemm_f32_with_variant(-1, act, static_cast<const float*>(A),
+                                         static_cast<const float*>(B), bias, static_cast<float*>(C),
+                                         M, N, K, static_cast<hipStream_t>(stream));
     if (M == 0 || N == 0) return JH_OK;
     if (!C || (K > 0 && (!A || !B))) return fail(JH_ERR_NULL, "gemm: null A, B or C");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (dtype == JH_F32) {
-        if (!aligned(A, 4) || !aligned(B, 4) || !aligned(C, 4) || !aligned(bias, 4))
-            return fail(JH_ERR_ALIGN, "gemm f32: operands must be 4-byte aligned");
-        return check_hip(jh::launch_gemm_f32(act, static_cast<const float*>(A),
-                                             static_cast<const float*>(B), bias,
-                                             static_cast<float*>(C), M, N, K, s),
-                         "gemm f32 launch");
-    }
     if (M % 8 || N % 8 || K % 8)
         return fail(JH_ERR_UNSUPPORTED, "gemm bf16: M, N, K must be multiples of 8 (got %d %d %d)",
                     M, N, K);
@@ -107,6 +127,47 @@ int jules_hip_gemm_bias_act(int dtype, int act, const void* A, const void* B, co
                                           static_cast<const uint16_t*>(B), bias,
                                           static_cast<uint16_t*>(C), M, N, K, s),
                      "gemm bf16 launch");
+}
+
+int jules_hip_gemm_tile(int dtype, int M, int N, int K, int* out) {
+    if (!out) return fail(JH_ERR_NULL, "gemm_tile: null out");
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "gemm_tile: M=%d N=%d K=%d", M, N, K);
+    if (dtype != JH_F32 && dtype != JH_BF16) return fail(JH_ERR_DTYPE, "gemm_tile: dtype %d", dtype);
+    const jh::GemmTile t = dtype == JH_F32 ? jh::f32_gemm_tile(M, N, K) : jh::bf16_gemm_tile(M, N, K);
+    out[0] = t.variant;
+    out[1] = t.tile_m;
+    out[2] = t.tile_n;
+    out[3] = t.tile_k;
+    return JH_OK;
+}
+
+int jules_hip_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float* A,
+                    int lda, const float* B, int ldb, float beta, float* C, int ldc, void* stream) {
+    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1))
+        return fail(JH_ERR_ARG, "sgemm: transA/transB must be 0 or 1 (got %d, %d)", transA, transB);
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "sgemm: M=%d N=%d K=%d", M, N, K);
+    // BLAS leading-dimension rules for row-major storage
+    const int a_cols = transA ? M : K, b_cols = transB ? K : N;
+    if (lda < (a_cols > 1 ? a_cols : 1) || ldb < (b_cols > 1 ? b_cols : 1) || ldc < (N > 1 ? N : 1))
+        return fail(JH_ERR_SHAPE, "sgemm: lda=%d ldb=%d ldc=%d below the row lengths %d %d %d", lda,
+                    ldb, ldc, a_cols, b_cols, N);
+    const int64_t a_rows = transA ? K : M, b_rows = transB ? N : K;
+    if (a_rows * lda > kMaxElems || b_rows * ldb > kMaxElems || (int64_t)M * ldc > kMaxElems)
+        return fail(JH_ERR_SHAPE, "sgemm: too large");
+    if (M == 0 || N == 0) return JH_OK;
+    const bool product = K > 0 && alpha != 0.0f;
+    if (!C || (product && (!A || !B))) return fail(JH_ERR_NULL, "sgemm: null A, B or C");
+    if (!aligned(A, 4) || !aligned(B, 4) || !aligned(C, 4))
+        return fail(JH_ERR_ALIGN, "sgemm: operands must be 4-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // The call LLVMBackend emits (LLVMBackend.cpp:1242-1255): plain C = A B
+    // on dense operands.  It runs the fp32 fma-chain GEMM, whose bits equal
+    // the reference's tiledMatmulWithActivation.
+    if (!transA && !transB && alpha == 1.0f && beta == 0.0f && lda == K && ldb == N && ldc == N)
+        return check_hip(jh::launch_gemm_f32(JH_ACT_NONE, A, B, nullptr, C, M, N, K, s),
+                         "sgemm launch");
+    return check_hip(jh::launch_sgemm(transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s),
+                     "sgemm launch");
 }
 
 int jules_hip_activation(int act, float* out, const float* in, int64_t n, void* stream) {
@@ -213,7 +274,8 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W, const
 int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                           float scale_A, float scale_B, const float* bias, void* stream) {
     if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "matmulInt8: M=%d N=%d K=%d", M, N, K);
-    if (K > 131072) return fail(JH_ERR_SHAPE, "matmulInt8: K=%d exceeds exact int32 range", K);
+    // |sum| <= K * 128 * 128 < 2^31 for K <= 131071: the int32 sum is exact
+    if (K > kMaxInt8K) return fail(JH_ERR_SHAPE, "matmulInt8: K=%d exceeds exact int32 range", K);
     if ((int64_t)M * K > kMaxElems || (int64_t)K * N > kMaxElems || (int64_t)M * N > kMaxElems)
         return fail(JH_ERR_SHAPE, "matmulInt8: too large");
     if (M == 0 || N == 0) return JH_OK;
@@ -228,7 +290,7 @@ int jules_hip_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M, int
                           const float* scale_A, const float* scale_B, const float* bias,
                           void* stream) {
     if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "matmulW8A8: M=%d N=%d K=%d", M, N, K);
-    if (K > 131072) return fail(JH_ERR_SHAPE, "matmulW8A8: K=%d exceeds exact int32 range", K);
+    if (K > kMaxInt8K) return fail(JH_ERR_SHAPE, "matmulW8A8: K=%d exceeds exact int32 range", K);
     if ((int64_t)M * K > kMaxElems || (int64_t)K * N > kMaxElems || (int64_t)M * N > kMaxElems)
         return fail(JH_ERR_SHAPE, "matmulW8A8: too large");
     if (M == 0 || N == 0) return JH_OK;
@@ -493,30 +555,14 @@ int k_attn_causal(int ni, const jh_tensor* in, int no, jh_tensor* out, const cha
     return attention_desc(1, ni, in, no, out, c, s);
 }
 
-// One workspace per device (W8A16 partials, cross-entropy row losses), grown
-// on demand, for callers of the registry who cannot pass one.  Guarded by a mutex; calls that share a
-// device through this path are serialised by the caller's stream order.
-std::mutex g_ws_mu;
-void* g_ws[64];
-size_t g_ws_bytes[64];
-
-int registry_workspace(size_t need, void** ws) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-        return fail(JH_ERR_HIP, "registry workspace: hipGetDevice");
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    if (g_ws_bytes[dev] < need) {
-        if (g_ws[dev]) (void)hipFree(g_ws[dev]);
-        g_ws[dev] = nullptr;
-        g_ws_bytes[dev] = 0;
-        void* p = nullptr;
-        if (hipMalloc(&p, need) != hipSuccess) return fail(JH_ERR_HIP, "registry workspace: hipMalloc");
-        if (hipMemset(p, 0, need) != hipSuccess) return fail(JH_ERR_HIP, "registry workspace: hipMemset");
-        g_ws[dev] = p;
-        g_ws_bytes[dev] = need;
-    }
-    *ws = g_ws[dev];
-    return JH_OK;
+// Workspace for registry callers, who cannot pass one (W8A16 partials and
+// flags, cross-entropy row losses, MLP activations): the library's buffer
+// for the caller's (device, stream), grown on demand.  Calls on one stream
+// run in stream order and may share it; calls on another stream get their
+// own buffer, so registry calls on two streams of one device do not race.
+int registry_workspace(size_t need, void* stream, void** ws) {
+    return check_hip(jh::stream_workspace(need, static_cast<hipStream_t>(stream), ws),
+                     "registry workspace");
 }
 
 int k_w8a16_silu(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void* s) {
@@ -541,7 +587,7 @@ int k_w8a16_silu(int ni, const jh_tensor* in, int no, jh_tensor* out, const char
     const size_t need = jules_hip_w8a16_workspace_size((int)M, (int)N, (int)K);
     void* ws = nullptr;
     if (need) {
-        const int st = registry_workspace(need, &ws);
+        const int st = registry_workspace(need, s, &ws);
         if (st != JH_OK) return st;
     }
     return jules_hip_w8a16_gemm_bias_act(JH_ACT_SILU, addr(x), static_cast<const int8_t*>(addr(w)),
@@ -616,7 +662,7 @@ int k_softmax(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, 
     if (ni != 1 || no != 1 || !in || !out) return fail(JH_ERR_ARG, "fusedSoftmax: (x) -> y");
     const jh_tensor& x = in[0];
     jh_tensor& y = out[0];
-    if (x.rank < 1 || !contiguous(x) || !contiguous(y) || numel(x) != numel(y) ||
+    if (x.rank < 1 || y.rank < 1 || !contiguous(x) || !contiguous(y) || numel(x) != numel(y) ||
         y.sizes[y.rank - 1] != x.sizes[x.rank - 1])
         return fail(JH_ERR_SHAPE, "fusedSoftmax: contiguous x and y of one shape");
     if (x.dtype != JH_F32 || y.dtype != JH_F32) return fail(JH_ERR_DTYPE, "fusedSoftmax: fp32");
@@ -661,7 +707,7 @@ int k_cross_entropy(int ni, const jh_tensor* in, int no, jh_tensor* out, const c
     if (M > INT32_MAX || N > INT32_MAX) return fail(JH_ERR_SHAPE, "fusedCrossEntropyLoss: too large");
     const size_t need = jules_hip_cross_entropy_workspace_size((int)M);
     void* ws = nullptr;
-    const int st = registry_workspace(need, &ws);
+    const int st = registry_workspace(need, s, &ws);
     if (st != JH_OK) return st;
     return jules_hip_cross_entropy(static_cast<const float*>(addr(x)),
                                    static_cast<const int32_t*>(addr(t)),
@@ -689,7 +735,7 @@ int k_mlp_forward(int ni, const jh_tensor* in, int no, jh_tensor* out, const cha
     const size_t need = jules_hip_mlp_forward_workspace_size((int)M, (int)K1, (int)N1, (int)N2);
     void* ws = nullptr;
     if (need > 0) {
-        const int st = registry_workspace(need, &ws);
+        const int st = registry_workspace(need, s, &ws);
         if (st != JH_OK) return st;
     }
     return jules_hip_mlp_forward(static_cast<const float*>(addr(x)), static_cast<const float*>(addr(w1)),
@@ -724,7 +770,7 @@ int k_mlp(int ni, const jh_tensor* in, int no, jh_tensor* out, const char*, void
     const size_t need = jules_hip_mlp_workspace_size((int)M, (int)K1, (int)N1, (int)N2);
     void* ws = nullptr;
     if (need > 0) {
-        const int st = registry_workspace(need, &ws);
+        const int st = registry_workspace(need, s, &ws);
         if (st != JH_OK) return st;
     }
     float* f[7];

@@ -30,11 +30,13 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "tiles.hpp"
 
 namespace jh {
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64;
+static_assert(BM == kBf16Tile && BN == kBf16Tile && BK == kBf16RegK, "tile table (tiles.hpp)");
 constexpr int THREADS = 256;
 constexpr int TILE_BYTES = 256 * BK * 2;  // one operand tile in LDS: 32 KiB
 constexpr int STAGE_BYTES = 2 * TILE_BYTES;
@@ -231,6 +233,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_kernel(
 // the register-staged kernel above.
 // ---------------------------------------------------------------------------
 constexpr int DBK = 32;                   // k per stage
+static_assert(DBK == kBf16DmaK, "tile table (tiles.hpp)");
 constexpr int NSTAGE = 4;
 constexpr int DTILE = 256 * DBK * 2;      // one operand stage: 16 KiB
 constexpr int DSTAGE = 2 * DTILE;         // A then B
@@ -493,7 +496,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_bf16_dma_kernel(
 hipError_t launch_gemm_bf16(int act, const uint16_t* A, const uint16_t* B, const float* bias,
                             uint16_t* C, int M, int N, int K, hipStream_t s) {
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    const bool full = M % BM == 0 && N % BN == 0 && K % DBK == 0 && K > 0;
+    const bool full = bf16_gemm_tile(M, N, K).variant == GV_BF16_DMA;
     hipError_t e = hipSuccess;
     JH_DISPATCH_ACT(act, ACT, {
         if (full)

@@ -18,6 +18,7 @@
 // extra fma(0, b, acc) could turn a -0 partial sum into +0).
 #include "common.hpp"
 #include "launch.hpp"
+#include "tiles.hpp"
 
 namespace jh {
 namespace {
@@ -118,9 +119,9 @@ __global__ __launch_bounds__((BM / TM) * (BN / TN)) void gemm_f32_kernel(
 // ring of PB groups of KU rows in flight per wave.  Every output is still one
 // fma chain over k = 0..K-1 in order.  At 512^3: 21.7 us (the 32x32 LDS-tiled
 // kernel 32.6 us); 1 or 4 rows per wave measured 27.1 and 26.8 us.
-constexpr int RWV = 4;   // waves per workgroup (4 x RW rows x 64 columns)
-constexpr int KU = 4;    // k per group (one ds_read_b128 of A per row)
-constexpr int ROWS_MAX_K = 2048;  // RW * RWV rows of K floats in LDS: 64 KiB at RW = 2
+constexpr int RWV = kF32RowsWaves;     // waves per workgroup (4 x RW rows x 64 columns)
+constexpr int KU = 4;                  // k per group (one ds_read_b128 of A per row)
+constexpr int ROWS_MAX_K = kF32RowsMaxK;  // RW * RWV rows of K floats in LDS: 64 KiB at RW = 2
 
 template <int ACT, int RW>  // RW rows per wave
 __global__ __launch_bounds__(64 * RWV) void gemm_f32_rows_kernel(
@@ -221,35 +222,49 @@ __global__ void activation_kernel(float* out, const float* __restrict__ in, int6
         out[i] = activate<ACT>(in[i]);
 }
 
+// fusedGelu (reference FusedKernels.h:606-627): gelu_zmm on the full groups
+// of 16 elements, and on the last partial group (the n % 16 elements from
+// n & ~15 on) the scalar formula with libm tanhf and x*x*x evaluated left to
+// right, as the reference's tail loop does.
+__global__ void fused_gelu_kernel(float* out, const float* __restrict__ in, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t nv = n & ~int64_t(15);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float x = in[i];
+        out[i] = i < nv ? gelu(x)
+                        : 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+    }
+}
+
 }  // namespace
+
+hipError_t launch_gemm_f32_variant(int variant, int act, const float* A, const float* B,
+                                   const float* bias, float* C, int M, int N, int K,
+                                   hipStream_t s) {
+    hipError_t e = hipSuccess;
+    auto rows = [&](auto kern, int rw) {
+        dim3 grid((N + 63) / 64, (M + rw * RWV - 1) / (rw * RWV));
+        const size_t lds = (size_t)rw * RWV * ((K + 3) & ~3) * sizeof(float);
+        hipLaunchKernelGGL(kern, grid, dim3(64 * RWV), lds, s, A, B, bias, C, M, N, K);
+        return hipGetLastError();
+    };
+    switch (variant) {
+    case GV_F32_ROWS1: JH_DISPATCH_ACT(act, ACT, e = rows(gemm_f32_rows_kernel<ACT, 1>, 1)); break;
+    case GV_F32_ROWS2: JH_DISPATCH_ACT(act, ACT, e = rows(gemm_f32_rows_kernel<ACT, 2>, 2)); break;
+    case GV_F32_T32:
+        JH_DISPATCH_ACT(act, ACT, e = (run<32, 32, kF32SliceK, 2, 2, ACT>(A, B, bias, C, M, N, K, s)));
+        break;
+    case GV_F32_T64:
+        JH_DISPATCH_ACT(act, ACT, e = (run<64, 64, kF32SliceK, 4, 4, ACT>(A, B, bias, C, M, N, K, s)));
+        break;
+    default: e = hipErrorInvalidValue;
+    }
+    return e;
+}
 
 hipError_t launch_gemm_f32(int act, const float* A, const float* B, const float* bias, float* C,
                            int M, int N, int K, hipStream_t s) {
-    // 64x64 tiles (4x4 per thread) once there are enough of them to cover the
-    // 256 CUs twice over; 32x32 tiles (2x2 per thread) for small problems such
-    // as 512^3, which then still launches 256 workgroups.
-    const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
-    hipError_t e = hipSuccess;
-    if ((int64_t)M * N <= (1 << 20) && K <= ROWS_MAX_K) {
-        // up to 1M outputs: the row-wave kernel, 2 rows per wave (8192 waves at
-        // most), or 1 row per wave when 2 would leave fewer than 1024 waves
-        // (at 512^3: 21.7 us at 2 rows, 27.1 us at 1 row)
-        const bool one = (int64_t)((N + 63) / 64) * ((M + 1) / 2) < 1024;
-        auto launch = [&](auto kern, int rw) {
-            dim3 grid((N + 63) / 64, (M + rw * RWV - 1) / (rw * RWV));
-            const size_t lds = (size_t)rw * RWV * ((K + 3) & ~3) * sizeof(float);
-            hipLaunchKernelGGL(kern, grid, dim3(64 * RWV), lds, s, A, B, bias, C, M, N, K);
-            return hipGetLastError();
-        };
-        JH_DISPATCH_ACT(act, ACT, {
-            e = one ? launch(gemm_f32_rows_kernel<ACT, 1>, 1) : launch(gemm_f32_rows_kernel<ACT, 2>, 2);
-        });
-    } else if (tiles64 >= 512) {
-        JH_DISPATCH_ACT(act, ACT, e = (run<64, 64, 32, 4, 4, ACT>(A, B, bias, C, M, N, K, s)));
-    } else {
-        JH_DISPATCH_ACT(act, ACT, e = (run<32, 32, 32, 2, 2, ACT>(A, B, bias, C, M, N, K, s)));
-    }
-    return e;
+    return launch_gemm_f32_variant(f32_gemm_tile(M, N, K).variant, act, A, B, bias, C, M, N, K, s);
 }
 
 hipError_t launch_activation(int act, float* out, const float* in, int64_t n, hipStream_t s) {
@@ -257,6 +272,10 @@ hipError_t launch_activation(int act, float* out, const float* in, int64_t n, hi
     const int threads = 256;
     int64_t blocks = (n + threads - 1) / threads;
     if (blocks > 4096) blocks = 4096;
+    if (act == JH_ACT_GELU) {
+        hipLaunchKernelGGL(fused_gelu_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, out, in, n);
+        return hipGetLastError();
+    }
     hipError_t e = hipSuccess;
     JH_DISPATCH_ACT(act, ACT, {
         hipLaunchKernelGGL(activation_kernel<ACT>, dim3((unsigned)blocks), dim3(threads), 0, s,

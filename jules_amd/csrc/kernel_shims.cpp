@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <limits>
 #include <string>
@@ -12,6 +13,8 @@
 
 #include "jules_hip.h"
 #include "jules_hip_kernel.hpp"
+#include "launch.hpp"
+#include "tiles.hpp"
 
 namespace jules {
 namespace kernel {
@@ -75,20 +78,36 @@ private:
     bool ok_ = true;
 };
 
+// variant: a kernel of the tile table, or -1 for the table's default
 void run_gemm(const float* A, const float* B, const float* bias, float* C, int M, int N, int K,
-              int act) {
+              int act, int variant = -1) {
     if (M < 0 || N < 0 || K < 0) return record(JH_ERR_SHAPE);
     DevBuf a(A, sizeof(float) * (size_t)M * K, true, false);
     DevBuf b(B, sizeof(float) * (size_t)K * N, true, false);
     DevBuf bi(bias, bias ? sizeof(float) * (size_t)N : 0, true, false);
     DevBuf c(C, sizeof(float) * (size_t)M * N, false, true);
     if (!a.ok() || !b.ok() || !bi.ok() || !c.ok()) return record(JH_ERR_HIP);
-    int st = jules_hip_gemm_bias_act(JH_F32, act, a.get(), b.get(),
-                                     static_cast<const float*>(bi.get()), c.get(), M, N, K, nullptr);
+    int st = jh::gemm_f32_with_variant(variant, act, static_cast<const float*>(a.get()),
+                                       static_cast<const float*>(b.get()),
+                                       static_cast<const float*>(bi.get()),
+                                       static_cast<float*>(c.get()), M, N, K, nullptr);
     if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
     if (st == JH_OK && !c.finish()) st = JH_ERR_HIP;
     record(st);
 }
+
+// the table kernel a TileConfig names at depth K, or -1
+int variant_of(const TileConfig& cfg, int K) {
+    for (int v = jh::GV_F32_ROWS1; v <= jh::GV_F32_T64; ++v) {
+        const jh::GemmTile t = jh::f32_variant_tile(v, K);
+        if (jh::f32_variant_valid(v, K) && t.tile_m == cfg.tile_m && t.tile_n == cfg.tile_n &&
+            t.tile_k == cfg.tile_k)
+            return v;
+    }
+    return -1;
+}
+
+TileConfig to_config(const jh::GemmTile& t) { return TileConfig{t.tile_m, t.tile_n, t.tile_k}; }
 
 void run_attention(float* out, const float* Q, const float* K, const float* V, int B, int H,
                    int S, int D) {
@@ -133,14 +152,66 @@ CacheInfo CacheInfo::detect() {
 
 TilePlanner::TilePlanner(const CacheInfo& cache) : cache_(cache) {}
 
-// The gfx950 tile table used by libjules_hip: fp32 SIMT tiles 64x64x16
-// (32x32x16 when fewer than 512 such tiles exist); bf16 MFMA tiles 256x256x64.
-TileConfig TilePlanner::computeAnalytical(int M, int N, int) const {
-    const long tiles64 = (long)((M + 63) / 64) * ((N + 63) / 64);
-    if (tiles64 >= 512) return TileConfig{64, 64, 16};
-    return TileConfig{32, 32, 16};
+TileConfig TilePlanner::computeAnalytical(int M, int N, int K) const {
+    return to_config(jh::f32_gemm_tile(M, N, K));
 }
-TileConfig TilePlanner::getTileConfig(int M, int N, int K) { return computeAnalytical(M, N, K); }
+
+TileConfig TilePlanner::getTileConfig(int M, int N, int K) {
+    for (const Entry& e : configCache_)
+        if (e.m == M && e.n == N && e.k == K) return e.cfg;
+    TileConfig cfg = computeAnalytical(M, N, K);
+    if (autoTune_ && M >= 32 && N >= 32) cfg = autoTune(M, N, K, cfg);  // TilePlanner.h:88-90
+    configCache_.push_back(Entry{M, N, K, cfg});
+    return cfg;
+}
+
+// Times each table kernel that can run the shape (TilePlanner.h:158-236 does
+// the same over CPU tile candidates): zero-filled device operands, one
+// warm-up and 10 timed launches per kernel between HIP events.  Any HIP
+// failure keeps the table's default.
+TileConfig TilePlanner::autoTune(int M, int N, int K, const TileConfig& defaultConfig) {
+    float *A = nullptr, *B = nullptr, *C = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    const size_t fa = (size_t)M * K, fb = (size_t)K * N, fc = (size_t)M * N;
+    TileConfig best = defaultConfig;
+    float best_ms = 0.0f;
+    bool ok = hipMalloc(&A, 4 * (fa ? fa : 1)) == hipSuccess &&
+              hipMalloc(&B, 4 * (fb ? fb : 1)) == hipSuccess &&
+              hipMalloc(&C, 4 * (fc ? fc : 1)) == hipSuccess &&
+              hipMemset(A, 0, 4 * (fa ? fa : 1)) == hipSuccess &&
+              hipMemset(B, 0, 4 * (fb ? fb : 1)) == hipSuccess &&
+              hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess;
+    for (int v = jh::GV_F32_ROWS1; ok && v <= jh::GV_F32_T64; ++v) {
+        if (!jh::f32_variant_valid(v, K)) continue;
+        constexpr int iters = 10;
+        ok = jh::launch_gemm_f32_variant(v, JH_ACT_NONE, A, B, nullptr, C, M, N, K, nullptr) ==
+                 hipSuccess &&
+             hipEventRecord(e0, nullptr) == hipSuccess;
+        for (int i = 0; ok && i < iters; ++i)
+            ok = jh::launch_gemm_f32_variant(v, JH_ACT_NONE, A, B, nullptr, C, M, N, K, nullptr) ==
+                 hipSuccess;
+        float ms = 0.0f;
+        ok = ok && hipEventRecord(e1, nullptr) == hipSuccess &&
+             hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+        if (ok && (best_ms == 0.0f || ms < best_ms)) {
+            best_ms = ms;
+            best = to_config(jh::f32_variant_tile(v, K));
+        }
+    }
+    if (!ok) {
+        (void)hipGetLastError();
+        best = defaultConfig;
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (A) (void)hipFree(A);
+    if (B) (void)hipFree(B);
+    if (C) (void)hipFree(C);
+    if (verbose_ && ok)
+        std::printf("Auto-tune [%d,%d]x[%d,%d]: tile=(%d,%d,%d) %.3fms\n", M, K, K, N, best.tile_m,
+                    best.tile_n, best.tile_k, best_ms / 10.0f);
+    return best;
+}
 
 ExecutionArena::ExecutionArena(size_t maxSize) : maxSize_(maxSize) {
     void* p = nullptr;
@@ -180,8 +251,27 @@ void fusedMatmulBiasRelu(const float* X, const float* W, const float* bias, floa
 }
 
 void tiledMatmulWithActivation(const float* A, const float* B, float* C, int M, int N, int K,
-                               const TileConfig&, ActivationType act) {
-    run_gemm(A, B, nullptr, C, M, N, K, static_cast<int>(act));
+                               const TileConfig& cfg, ActivationType act) {
+    run_gemm(A, B, nullptr, C, M, N, K, static_cast<int>(act), variant_of(cfg, K));
+}
+
+void blasMatmul(const float* A, const float* B, float* C, int M, int N, int K, float alpha,
+                float beta, bool transA, bool transB) {
+    if (M < 0 || N < 0 || K < 0) return record(JH_ERR_SHAPE);
+    const size_t f = sizeof(float);
+    DevBuf a(A, f * (size_t)M * K, true, false), b(B, f * (size_t)K * N, true, false);
+    // C is read when beta != 0 (FusedKernels.h:637-643 passes beta to sgemm)
+    DevBuf c(C, f * (size_t)M * N, beta != 0.0f, true);
+    if (!a.ok() || !b.ok() || !c.ok()) return record(JH_ERR_HIP);
+    // leading dimensions as the reference passes them: transA ? M : K,
+    // transB ? K : N, N
+    int st = jules_hip_sgemm(transA ? 1 : 0, transB ? 1 : 0, M, N, K, alpha,
+                             static_cast<const float*>(a.get()), transA ? M : K,
+                             static_cast<const float*>(b.get()), transB ? K : N, beta,
+                             static_cast<float*>(c.get()), N, nullptr);
+    if (st == JH_OK && hipDeviceSynchronize() != hipSuccess) st = JH_ERR_HIP;
+    if (st == JH_OK && !c.finish()) st = JH_ERR_HIP;
+    record(st);
 }
 
 void fusedGelu(float* output, const float* input, int N) {
@@ -345,8 +435,11 @@ void flashAttention(float* output, const float* Q, const float* K, const float* 
 }
 
 void attention(float* output, const float* Q, const float* K, const float* V, int batch, int heads,
-               int seq, int head_dim, ExecutionArena&, TilePlanner&) {
-    run_attention(output, Q, K, V, batch, heads, seq, head_dim);
+               int seq, int head_dim, ExecutionArena& arena, TilePlanner& planner) {
+    if (shouldUseFlashAttention(seq, head_dim, planner.cacheInfo().l3_bytes))
+        flashAttention(output, Q, K, V, batch, heads, seq, head_dim, arena, planner);
+    else
+        standardAttention(output, Q, K, V, batch, heads, seq, head_dim, arena);
 }
 
 void standardAttention(float* output, const float* Q, const float* K, const float* V, int batch,

@@ -10,6 +10,20 @@ namespace jh {
 
 hipError_t launch_gemm_f32(int act, const float* A, const float* B, const float* bias,
                            float* C, int M, int N, int K, hipStream_t s);
+// one fp32 GEMM kernel of the tile table (tiles.hpp: GV_F32_*); the caller
+// has checked f32_variant_valid()
+hipError_t launch_gemm_f32_variant(int variant, int act, const float* A, const float* B,
+                                   const float* bias, float* C, int M, int N, int K,
+                                   hipStream_t s);
+// the fp32 GEMM entry point's validation and launch with a chosen table
+// variant (-1: the table's default), for jules::kernel::tiledMatmulWithActivation
+int gemm_f32_with_variant(int variant, int act, const float* A, const float* B, const float* bias,
+                          float* C, int M, int N, int K, hipStream_t s);
+// C = alpha op(A) op(B) + beta C, fp32 on MFMA (mlp.hip); op(X) = X^T when
+// the trans flag is set; row-major with leading dimensions lda, ldb, ldc
+hipError_t launch_sgemm(bool transA, bool transB, int M, int N, int K, float alpha, const float* A,
+                        int lda, const float* B, int ldb, float beta, float* C, int ldc,
+                        hipStream_t s);
 hipError_t launch_gemm_bf16(int act, const uint16_t* A, const uint16_t* B, const float* bias,
                             uint16_t* C, int M, int N, int K, hipStream_t s);
 hipError_t launch_activation(int act, float* out, const float* in, int64_t n, hipStream_t s);

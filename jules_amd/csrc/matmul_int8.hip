@@ -4,7 +4,7 @@
 // and its W8A8 form with per-token activation scales sA[i] and per-channel
 // weight scales sB[j] (the scale product rounded to fp32 per element):
 //   C[i,j] = float(sum_k A[i,k] * B[k,j]) * (sA[i] * sB[j])    [+ bias[j]]
-// int32 accumulation is exact (|sum| <= 127*128*K < 2^31 for K <= 131072), so
+// int32 accumulation is exact (|sum| <= 128*128*K < 2^31 for K <= 131071), so
 // any summation order gives the reference's integer; the epilogue is one fp32
 // multiply by the fp32-rounded scale product, then one add of bias.
 //

@@ -30,6 +30,7 @@
 // Out-of-range elements are loaded as 0 (any summation order is allowed
 // here: the reference's products are BLAS calls).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -46,11 +47,20 @@ constexpr int LDB_S = BN + 1;
 constexpr int PA = BM * BK / GT;     // A elements per thread per slice (8)
 constexpr int PB = BK * BN / GT;
 
+// BLAS sgemm epilogue: alpha * acc + beta * C, with C not read when
+// beta = 0 (so NaNs in an uninitialised C never propagate), and acc itself
+// when alpha = 1 and beta = 0
+__device__ __forceinline__ float alpha_beta(float acc, float alpha, float beta, const float* c) {
+    const float v = alpha * acc;
+    return beta == 0.0f ? v : v + beta * *c;
+}
+
 template <bool TA, bool TB, int EPI>
 __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
     const float* __restrict__ A, int lda, const float* __restrict__ B, int ldb,
     float* __restrict__ C, int ldc, int M, int N, int K, const float* __restrict__ bias,
-    const float* __restrict__ mask, int ldm, int kc, float* __restrict__ part) {
+    const float* __restrict__ mask, int ldm, int kc, float* __restrict__ part, float alpha,
+    float beta) {
     __shared__ float As[2][BK * LDA_S];
     __shared__ float Bs[2][BK * LDB_S];
 
@@ -169,6 +179,8 @@ __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
                     v = v > 0.0f ? v : 0.0f;
                 } else if constexpr (EPI == 3) {
                     v = mask[(int64_t)m * ldm + n] > 0.0f ? v : 0.0f;
+                } else if constexpr (EPI == 4) {
+                    v = alpha_beta(v, alpha, beta, C + (int64_t)m * ldc + n);
                 }
                 C[(int64_t)m * ldc + n] = v;
             }
@@ -179,7 +191,8 @@ __global__ __launch_bounds__(GT, 2) void gemm_f32_mfma_kernel(
 template <int EPI>
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
                                      float* __restrict__ C, int ldc, const float* __restrict__ bias,
-                                     const float* __restrict__ mask, int ldm) {
+                                     const float* __restrict__ mask, int ldm, float alpha,
+                                     float beta) {
     const int64_t total = (int64_t)M * N, stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
         const int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
@@ -192,8 +205,21 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int 
             v = v > 0.0f ? v : 0.0f;
         } else if constexpr (EPI == 3) {
             v = mask[(int64_t)m * ldm + n] > 0.0f ? v : 0.0f;
+        } else if constexpr (EPI == 4) {
+            v = alpha_beta(v, alpha, beta, C + (int64_t)m * ldc + n);
         }
         C[(int64_t)m * ldc + n] = v;
+    }
+}
+
+// C = beta * C (alpha * op(A) op(B) vanishes: K = 0 or alpha = 0); beta = 0
+// writes zeros without reading C, as BLAS does
+__global__ void scale_c_kernel(float* __restrict__ C, int ldc, int M, int N, float beta) {
+    const int64_t total = (int64_t)M * N, stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        const int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
+        float* c = C + (int64_t)m * ldc + n;
+        *c = beta == 0.0f ? 0.0f : beta * *c;
     }
 }
 
@@ -233,7 +259,7 @@ __global__ void fill_kernel(float* __restrict__ p, int64_t n, float v) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
 }
 
-enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RELU = 2, EPI_MASK = 3 };
+enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RELU = 2, EPI_MASK = 3, EPI_ALPHA_BETA = 4 };
 
 // Split-K plan: a GEMM with fewer than 128 output tiles gets its K range
 // split (at least 4 slices per split) so that about 256 workgroups run; the
@@ -260,16 +286,17 @@ size_t kplan_floats(int M, int N, int K) {
 
 template <bool TA, bool TB, int EPI>
 hipError_t gemm(const float* A, int lda, const float* B, int ldb, float* C, int ldc, int M, int N,
-                int K, const float* bias, const float* mask, int ldm, float* part, hipStream_t s) {
+                int K, const float* bias, const float* mask, int ldm, float* part, hipStream_t s,
+                float alpha = 1.0f, float beta = 0.0f) {
     const KPlan p = kplan(M, N, K);
     const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, p.S);
     hipLaunchKernelGGL((gemm_f32_mfma_kernel<TA, TB, EPI>), grid, dim3(GT), 0, s, A, lda, B, ldb, C,
-                       ldc, M, N, K, bias, mask, ldm, p.kc, p.S > 1 ? part : nullptr);
+                       ldc, M, N, K, bias, mask, ldm, p.kc, p.S > 1 ? part : nullptr, alpha, beta);
     if (p.S > 1) {
         int64_t b = ((int64_t)M * N + 255) / 256;
         if (b > 2048) b = 2048;
         hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3((unsigned)b), dim3(256), 0, s, part, p.S,
-                           M, N, C, ldc, bias, mask, ldm);
+                           M, N, C, ldc, bias, mask, ldm, alpha, beta);
     }
     return hipGetLastError();
 }
@@ -396,6 +423,37 @@ hipError_t launch_mlp_forward_backward(const float* X, const float* W1, const fl
     if (dX && (e = gemm<false, true, EPI_NONE>(dH, N1, W1, N1, dX, K1, M, K1, N1, nullptr, nullptr, 0, kpart, s)))
         return e;
     return hipSuccess;
+}
+
+// blasMatmul / cblas_sgemm (reference FusedKernels.h:633-644): the MFMA GEMM
+// above with the sgemm epilogue.  Skinny products split K into a per-stream
+// library buffer (the entry point has no workspace argument).
+hipError_t launch_sgemm(bool transA, bool transB, int M, int N, int K, float alpha, const float* A,
+                        int lda, const float* B, int ldb, float beta, float* C, int ldc,
+                        hipStream_t s) {
+    if (M == 0 || N == 0) return hipSuccess;
+    if (K == 0 || alpha == 0.0f) {
+        int64_t b = ((int64_t)M * N + 255) / 256;
+        if (b > 4096) b = 4096;
+        hipLaunchKernelGGL(scale_c_kernel, dim3((unsigned)b), dim3(256), 0, s, C, ldc, M, N, beta);
+        return hipGetLastError();
+    }
+    float* part = nullptr;
+    const size_t pf = kplan_floats(M, N, K);
+    if (pf) {
+        void* ws = nullptr;
+        const hipError_t e = stream_workspace(pf * sizeof(float), s, &ws);
+        if (e != hipSuccess) return e;
+        part = static_cast<float*>(ws);
+    }
+    auto run = [&](auto ta, auto tb) {
+        return gemm<decltype(ta)::value, decltype(tb)::value, EPI_ALPHA_BETA>(
+            A, lda, B, ldb, C, ldc, M, N, K, nullptr, nullptr, 0, part, s, alpha, beta);
+    };
+    using F = std::false_type;
+    using T = std::true_type;
+    if (transA) return transB ? run(T{}, T{}) : run(T{}, F{});
+    return transB ? run(F{}, T{}) : run(F{}, F{});
 }
 
 }  // namespace jh

@@ -287,7 +287,7 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
 // A lane loads 16 consecutive columns of 16 consecutive B rows, transposes
 // the 16x16 bytes in registers (v_perm_b32, 4x4 blocks) and feeds column j
 // as the B operand of v_mfma_i32_16x16x64_i8 with A (M padded to 16) as the
-// A operand.  Partials are int32 (exact for K <= 131072), summed in split
+// A operand.  Partials are int32 (exact for K <= 131071), summed in split
 // order by the last workgroup of the column tile, which applies the epilogue
 // C = float(sum) * (sA * sB) + bias of matmulInt8's scalar path.
 // ---------------------------------------------------------------------------

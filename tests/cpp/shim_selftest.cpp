@@ -1,0 +1,345 @@
+// shim_selftest.cpp - drives the jules::kernel C++ entry points of
+// include/jules_hip_kernel.hpp the way the reference's caller does
+// (benchmarks/bench_kernel.cpp:141,148,155,242,545): synchronous calls on
+// caller-owned buffers.  Each hot-path entry point runs with host buffers
+// (the library stages them through the GPU), with device buffers (used in
+// place), and in place (output == input) where the reference allows it.
+//
+// Usage: shim_selftest DIR.  DIR holds the seeded inputs as raw
+// little-endian arrays written by tests/test_gpu_shims.py (names and shapes
+// below); every result is written back to DIR as <case>.bin for that test to
+// compare with the oracle.  The planner, arena and selector checks that need
+// no oracle run here.  Prints "shim selftest ok" and exits 0 when every
+// call returned JH_OK and every check held.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "jules_hip_kernel.hpp"
+
+using namespace jules::kernel;
+
+// shapes shared with tests/test_gpu_shims.py
+constexpr int GM = 67, GN = 80, GK = 45;       // GEMM
+constexpr int GELU_N = 1000;                   // 1000 % 16 = 8: a scalar tail
+constexpr int RM = 37, RN = 100;               // row kernels (100 % 16 = 4)
+constexpr int AB = 2, AH = 3, AS = 100, AD = 64;  // attention [B,H,S,D]
+constexpr int I1M = 8, I1N = 96, I1K = 256;    // matmulInt8, decode path
+constexpr int I2M = 40, I2N = 70, I2K = 200;   // matmulInt8, general path
+
+static std::string g_dir;
+static int g_fail = 0;
+
+#define CHECK(c)                                                       \
+    do {                                                               \
+        if (!(c)) {                                                    \
+            std::printf("FAIL %s:%d: %s\n", __FILE__, __LINE__, #c);    \
+            ++g_fail;                                                  \
+        }                                                              \
+    } while (0)
+
+static void step(const char* name) {
+    std::printf("[case] %s\n", name);
+    std::fflush(stdout);
+}
+
+template <typename T>
+static std::vector<T> load(const char* name, size_t n) {
+    std::vector<T> v(n);
+    FILE* f = std::fopen((g_dir + "/" + name + ".bin").c_str(), "rb");
+    if (!f || std::fread(v.data(), sizeof(T), n, f) != n) {
+        std::printf("FAIL cannot read %s (%zu elements)\n", name, n);
+        ++g_fail;
+    }
+    if (f) std::fclose(f);
+    return v;
+}
+
+template <typename T>
+static void save(const std::string& name, const T* p, size_t n) {
+    FILE* f = std::fopen((g_dir + "/" + name + ".bin").c_str(), "wb");
+    if (!f || std::fwrite(p, sizeof(T), n, f) != n) {
+        std::printf("FAIL cannot write %s\n", name.c_str());
+        ++g_fail;
+    }
+    if (f) std::fclose(f);
+}
+
+template <typename T>
+static void save(const std::string& name, const std::vector<T>& v) {
+    save(name, v.data(), v.size());
+}
+
+// device copy of a host vector; freed by the caller
+template <typename T>
+static T* to_dev(const std::vector<T>& v) {
+    void* p = nullptr;
+    if (hipMalloc(&p, sizeof(T) * (v.size() ? v.size() : 1)) != hipSuccess ||
+        hipMemcpy(p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        std::printf("FAIL hipMalloc/hipMemcpy\n");
+        ++g_fail;
+    }
+    return static_cast<T*>(p);
+}
+
+template <typename T>
+static std::vector<T> from_dev(const T* p, size_t n) {
+    std::vector<T> v(n);
+    if (hipMemcpy(v.data(), p, sizeof(T) * n, hipMemcpyDeviceToHost) != hipSuccess) {
+        std::printf("FAIL hipMemcpy back\n");
+        ++g_fail;
+    }
+    return v;
+}
+
+static void ok_status(const char* what) {
+    if (lastStatus() != JH_OK) {
+        std::printf("FAIL %s: status %d (%s)\n", what, lastStatus(), lastError());
+        ++g_fail;
+    }
+}
+
+int main(int argc, char** argv) {
+    if (argc != 2) {
+        std::printf("usage: shim_selftest DIR\n");
+        return 2;
+    }
+    g_dir = argv[1];
+    const auto A = load<float>("gemm_A", GM * GK), B = load<float>("gemm_B", GK * GN);
+    const auto bias = load<float>("gemm_bias", GN), C0 = load<float>("gemm_C0", GM * GN);
+    const auto gx = load<float>("gelu_x", GELU_N);
+    const auto rx = load<float>("row_x", RM * RN), gamma = load<float>("ln_gamma", RN),
+               beta = load<float>("ln_beta", RN);
+    const auto tgt = load<int32_t>("ce_t", RM);
+    const size_t an = (size_t)AB * AH * AS * AD;
+    const auto q = load<float>("attn_q", an), k = load<float>("attn_k", an),
+               v = load<float>("attn_v", an);
+    const auto a1 = load<int8_t>("i8_A1", I1M * I1K), b1 = load<int8_t>("i8_B1", I1K * I1N);
+    const auto bias1 = load<float>("i8_bias1", I1N);
+    const auto a2 = load<int8_t>("i8_A2", I2M * I2K), b2 = load<int8_t>("i8_B2", I2K * I2N);
+    const auto bias2 = load<float>("i8_bias2", I2N);
+    if (g_fail) return 1;
+
+    // ---- TilePlanner: the table, then the on-GPU auto-tune ----------------
+    step("TilePlanner");
+    TilePlanner fixed;
+    fixed.setAutoTune(false);
+    TileConfig t = fixed.getTileConfig(512, 512, 512);
+    CHECK(t.tile_m == 8 && t.tile_n == 64 && t.tile_k == 512);  // row kernel, 2 rows per wave
+    t = fixed.computeAnalytical(64, 256, 784);
+    CHECK(t.tile_m == 4 && t.tile_n == 64 && t.tile_k == 784);  // 1 row per wave
+    t = fixed.computeAnalytical(4096, 4096, 4096);
+    CHECK(t.tile_m == 64 && t.tile_n == 64 && t.tile_k == 32);
+    TilePlanner tuned;  // auto-tune on, as the reference's default
+    const TileConfig tc = tuned.getTileConfig(GM, GN, GK);
+    ok_status("autotune");
+    const TileConfig table[4] = {{4, 64, 48}, {8, 64, 48}, {32, 32, 32}, {64, 64, 32}};
+    bool in_table = false;
+    for (const TileConfig& c : table)
+        in_table |= c.tile_m == tc.tile_m && c.tile_n == tc.tile_n && c.tile_k == tc.tile_k;
+    CHECK(in_table);
+    const TileConfig tc2 = tuned.getTileConfig(GM, GN, GK);  // cached
+    CHECK(tc2.tile_m == tc.tile_m && tc2.tile_n == tc.tile_n && tc2.tile_k == tc.tile_k);
+
+    // ---- GEMM shims --------------------------------------------------------
+    std::vector<float> out(GM * GN);
+    float *dA = to_dev(A), *dB = to_dev(B), *dbias = to_dev(bias), *dC = to_dev(out);
+    for (int act = 0; act <= 5; ++act) {
+        const std::string n = "gemm_act" + std::to_string(act);
+        step(n.c_str());
+        tiledMatmulWithActivation(A.data(), B.data(), out.data(), GM, GN, GK, tc,
+                                  static_cast<ActivationType>(act));
+        ok_status(n.c_str());
+        save(n + "_H", out);
+        tiledMatmulWithActivation(dA, dB, dC, GM, GN, GK, tc, static_cast<ActivationType>(act));
+        ok_status(n.c_str());
+        save(n + "_D", from_dev(dC, out.size()));
+    }
+    for (int i = 0; i < 4; ++i) {  // every kernel of the table: same bits
+        const std::string n = "gemm_var" + std::to_string(i);
+        step(n.c_str());
+        tiledMatmulWithActivation(A.data(), B.data(), out.data(), GM, GN, GK, table[i],
+                                  ActivationType::Gelu);
+        ok_status(n.c_str());
+        save(n, out);
+    }
+    step("fusedMatmulRelu");
+    fusedMatmulRelu(A.data(), B.data(), out.data(), GM, GK, GN);
+    ok_status("fusedMatmulRelu");
+    save("gemm_relu_H", out);
+    fusedMatmulRelu(dA, dB, dC, GM, GK, GN);
+    ok_status("fusedMatmulRelu device");
+    save("gemm_relu_D", from_dev(dC, out.size()));
+    step("fusedMatmulBiasRelu");
+    fusedMatmulBiasRelu(A.data(), B.data(), bias.data(), out.data(), GM, GK, GN);
+    ok_status("fusedMatmulBiasRelu");
+    save("gemm_bias_relu_H", out);
+    fusedMatmulBiasRelu(dA, dB, dbias, dC, GM, GK, GN);
+    ok_status("fusedMatmulBiasRelu device");
+    save("gemm_bias_relu_D", from_dev(dC, out.size()));
+
+    // blasMatmul: (alpha, beta, transA, transB).  With transA, gemm_A is read
+    // as [GK, GM]; with transB, gemm_B as [GN, GK].
+    struct Blas {
+        const char* name;
+        float alpha, beta;
+        bool ta, tb;
+    } blas[] = {{"blas_nn", 1.0f, 0.0f, false, false}, {"blas_ab", 0.5f, 2.0f, false, false},
+                {"blas_tn", 1.0f, 0.0f, true, false},  {"blas_nt", -1.5f, 0.0f, false, true},
+                {"blas_tt", 2.0f, -1.0f, true, true}};
+    for (const Blas& c : blas) {
+        step(c.name);
+        out = C0;
+        blasMatmul(A.data(), B.data(), out.data(), GM, GN, GK, c.alpha, c.beta, c.ta, c.tb);
+        ok_status(c.name);
+        save(std::string(c.name) + "_H", out);
+        float* dc = to_dev(C0);
+        blasMatmul(dA, dB, dc, GM, GN, GK, c.alpha, c.beta, c.ta, c.tb);
+        ok_status(c.name);
+        save(std::string(c.name) + "_D", from_dev(dc, out.size()));
+        (void)hipFree(dc);
+    }
+
+    // ---- fusedGelu: host, device, in place on both --------------------------
+    step("fusedGelu");
+    std::vector<float> g(GELU_N);
+    fusedGelu(g.data(), gx.data(), GELU_N);
+    ok_status("fusedGelu");
+    save("gelu_H", g);
+    g = gx;
+    fusedGelu(g.data(), g.data(), GELU_N);
+    ok_status("fusedGelu in place");
+    save("gelu_I", g);
+    float *dgx = to_dev(gx), *dg = to_dev(g);
+    fusedGelu(dg, dgx, GELU_N);
+    ok_status("fusedGelu device");
+    save("gelu_D", from_dev(dg, GELU_N));
+    fusedGelu(dgx, dgx, GELU_N);
+    ok_status("fusedGelu device in place");
+    save("gelu_DI", from_dev(dgx, GELU_N));
+
+    // ---- row kernels --------------------------------------------------------
+    step("fusedSoftmax");
+    std::vector<float> r(RM * RN);
+    fusedSoftmax(r.data(), rx.data(), RM, RN);
+    ok_status("fusedSoftmax");
+    save("softmax_H", r);
+    r = rx;
+    fusedSoftmax(r.data(), r.data(), RM, RN);
+    ok_status("fusedSoftmax in place");
+    save("softmax_I", r);
+    float* drx = to_dev(rx);
+    fusedSoftmax(drx, drx, RM, RN);
+    ok_status("fusedSoftmax device in place");
+    save("softmax_DI", from_dev(drx, r.size()));
+
+    step("fusedLayerNorm");
+    fusedLayerNorm(r.data(), rx.data(), gamma.data(), beta.data(), RM, RN);
+    ok_status("fusedLayerNorm");
+    save("layernorm_H", r);
+    float *drx2 = to_dev(rx), *dgam = to_dev(gamma), *dbet = to_dev(beta);
+    fusedLayerNorm(drx2, drx2, dgam, dbet, RM, RN, 1e-5f);
+    ok_status("fusedLayerNorm device in place");
+    save("layernorm_DI", from_dev(drx2, r.size()));
+
+    step("fusedCrossEntropyLoss");
+    float loss = fusedCrossEntropyLoss(rx.data(), tgt.data(), r.data(), RM, RN);
+    ok_status("fusedCrossEntropyLoss");
+    save("ce_grad_H", r);
+    save("ce_loss_H", &loss, 1);
+    r = rx;  // grad aliasing the logits, as the reference allows
+    loss = fusedCrossEntropyLoss(r.data(), tgt.data(), r.data(), RM, RN);
+    ok_status("fusedCrossEntropyLoss in place");
+    save("ce_grad_I", r);
+    save("ce_loss_I", &loss, 1);
+    float* drx3 = to_dev(rx);
+    int32_t* dt = to_dev(tgt);
+    loss = fusedCrossEntropyLoss(drx3, dt, drx3, RM, RN);
+    ok_status("fusedCrossEntropyLoss device in place");
+    save("ce_grad_DI", from_dev(drx3, r.size()));
+    save("ce_loss_DI", &loss, 1);
+
+    // ---- attention ----------------------------------------------------------
+    ExecutionArena arena(16 << 20);
+    TilePlanner planner;
+    std::vector<float> o(an);
+    step("flashAttention");
+    flashAttention(o.data(), q.data(), k.data(), v.data(), AB, AH, AS, AD, arena, planner);
+    ok_status("flashAttention");
+    save("flash_H", o);
+    float *dq = to_dev(q), *dk = to_dev(k), *dv = to_dev(v), *dout = to_dev(o);
+    flashAttention(dout, dq, dk, dv, AB, AH, AS, AD, arena, planner);
+    ok_status("flashAttention device");
+    save("flash_D", from_dev(dout, an));
+    step("attention");
+    attention(o.data(), q.data(), k.data(), v.data(), AB, AH, AS, AD, arena, planner);
+    ok_status("attention");
+    save("attention_H", o);
+    step("standardAttention");
+    standardAttention(o.data(), q.data(), k.data(), v.data(), AB, AH, AS, AD, arena);
+    ok_status("standardAttention");
+    save("standard_H", o);
+
+    // ---- matmulInt8 ---------------------------------------------------------
+    step("matmulInt8");
+    std::vector<float> c1(I1M * I1N), c2(I2M * I2N);
+    matmulInt8(a1.data(), b1.data(), c1.data(), I1M, I1N, I1K, 0.013f, 0.021f, bias1.data());
+    ok_status("matmulInt8 decode");
+    save("i8_1_H", c1);
+    matmulInt8(a2.data(), b2.data(), c2.data(), I2M, I2N, I2K, 0.5f, 0.25f);
+    ok_status("matmulInt8 general");
+    save("i8_2_H", c2);
+    int8_t *da1 = to_dev(a1), *db1 = to_dev(b1);
+    float *dbias1 = to_dev(bias1), *dc1 = to_dev(c1);
+    matmulInt8(da1, db1, dc1, I1M, I1N, I1K, 0.013f, 0.021f, dbias1, &arena);
+    ok_status("matmulInt8 device");
+    save("i8_1_D", from_dev(dc1, c1.size()));
+
+    // ---- ExecutionArena: allocate, align, overflow, reset ---------------------
+    step("ExecutionArena");
+    ExecutionArena small(1 << 20);
+    CHECK(small.capacity() == (1u << 20) && small.rawBuffer() != nullptr);
+    float* p0 = small.allocate<float>(1000);
+    CHECK(p0 == reinterpret_cast<float*>(small.rawBuffer()) && small.usedBytes() == 4000);
+    char* p1 = static_cast<char*>(small.allocateBytes(100));
+    CHECK(p1 == small.rawBuffer() + 4096 && small.usedBytes() == 4196);  // 256-byte aligned
+    CHECK(small.allocateBytes(2 << 20) == nullptr && lastStatus() == JH_ERR_WORKSPACE);
+    CHECK(small.usedBytes() == 4196 && small.highWaterMark() == 4196);
+    hipPointerAttribute_t attr;
+    CHECK(hipPointerGetAttributes(&attr, p0) == hipSuccess && attr.type == hipMemoryTypeDevice);
+    // arena memory serves as device buffers of a shim call
+    CHECK(hipMemcpy(p0, gx.data(), 4 * 1000, hipMemcpyHostToDevice) == hipSuccess);
+    fusedGelu(p0, p0, 1000);
+    ok_status("fusedGelu in arena memory");
+    save("gelu_arena", from_dev(p0, 1000));
+    small.reset();
+    CHECK(small.usedBytes() == 0 && small.highWaterMark() == 4196);
+    CHECK(small.allocate<float>(10) == p0);
+    small.resetAndZero();
+    const std::vector<float> zeros = from_dev(p0, 10);
+    for (float z : zeros) CHECK(z == 0.0f);
+
+    // ---- shouldUseFlashAttention (FusedKernels.h:1085-1115) ------------------
+    step("shouldUseFlashAttention");
+    CHECK(shouldUseFlashAttention(1024, 64, 256u << 20));        // S >= 64, D <= 256
+    CHECK(!shouldUseFlashAttention(32, 64, 256u << 20));         // small, fits
+    CHECK(shouldUseFlashAttention(32, 64, 1024));                // 4 KiB matrix > 1 KiB
+    CHECK(!shouldUseFlashAttention(128, 512, 256u << 20));       // head_dim > 256
+    CHECK(shouldUseFlashAttention(9000, 512, 256u << 20));       // 324 MB matrix
+
+    for (void* p : {(void*)dA, (void*)dB, (void*)dbias, (void*)dC, (void*)dgx, (void*)dg,
+                    (void*)drx, (void*)drx2, (void*)dgam, (void*)dbet, (void*)drx3, (void*)dt,
+                    (void*)dq, (void*)dk, (void*)dv, (void*)dout, (void*)da1, (void*)db1,
+                    (void*)dbias1, (void*)dc1})
+        (void)hipFree(p);
+    if (g_fail) {
+        std::printf("%d failures\n", g_fail);
+        return 1;
+    }
+    std::printf("shim selftest ok\n");
+    return 0;
+}

@@ -234,3 +234,105 @@ def test_mlp_forward_validation():
     bad[0] = P + 2  # X misaligned
     assert f(*bad) == ALIGN
     assert f(*([P] * 6 + [0, 3, 5, 2, None, 0, None])) == 0  # M = 0: nothing to do
+
+
+def test_flash_bwd_validation():
+    """Every case fails validation, so the placeholder addresses are never
+    dereferenced (this runs without a GPU)."""
+    f = _lib.lib().jules_hip_flash_attn_bwd
+    args = [1, 1, 0.125] + [P] * 9 + [1, 1, 16, 128, P, 1 << 20, None]
+    for idx, val, status in ((0, 0, UNSUP),        # fp32: not implemented
+                             (15, 160, UNSUP),     # head_dim > 128
+                             (15, 0, SHAPE),
+                             (17, 0, WS),          # workspace bytes
+                             (8, None, NULL),      # lse
+                             (3, P + 8, ALIGN),    # Q 16-byte alignment
+                             (1, 2, ARG),          # causal not 0/1
+                             (2, float("nan"), ARG)):
+        bad = list(args)
+        bad[idx] = val
+        assert f(*bad) == status, (idx, val)
+
+
+def test_int8_depth_limit():
+    """K <= 131071 keeps every int32 sum exact ((-128)^2 * 131071 < 2^31);
+    K = 131072 could reach 2^31 and is rejected before any launch."""
+    L = _lib.lib()
+    assert L.jules_hip_matmul_int8(P, P, P, 4, 16, 131072, 1.0, 1.0, None, None) == SHAPE
+    assert L.jules_hip_matmul_w8a8(P, P, P, 4, 16, 131072, None, P, None, None) == SHAPE
+    assert L.jules_hip_matmul_int8(None, P, P, 4, 16, 131071, 1.0, 1.0, None, None) == NULL
+
+
+def test_registry_softmax_rank0_output():
+    """A rank-0 output descriptor is rejected before its sizes are read."""
+    fn = _lib.lookup("fusedSoftmax")
+    x = (_lib.JhTensor * 1)()
+    y = (_lib.JhTensor * 1)()
+    x[0].data, x[0].rank, x[0].dtype = P, 1, 0
+    x[0].sizes[0], x[0].strides[0] = 1, 1
+    y[0].data, y[0].rank, y[0].dtype = P, 0, 0
+    assert fn(1, x, 1, y, None, None) == SHAPE
+
+
+CBLAS_LIB = os.path.join(ROOT, "jules_amd", "libjules_cblas.so")
+
+
+def test_cblas_symbols_in_their_own_library():
+    """cblas_sgemm lives in libjules_cblas.so only: loading libjules_hip.so
+    never interposes a BLAS for other callers."""
+    assert not any(s.startswith("cblas_") for s in _exported())
+    out = subprocess.run(["nm", "-D", "--defined-only", CBLAS_LIB], capture_output=True, text=True,
+                         check=True).stdout
+    syms = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert {"cblas_sgemm", "jules_cblas_last_status"} <= syms
+
+
+def test_cblas_dlopen_validation():
+    """A plain C caller binds cblas_sgemm through dlopen + a process-wide dlsym
+    (as the reference's ORC JIT resolves it) and gets every argument error as
+    a status, with C untouched and no device work."""
+    exe = os.path.join(ROOT, "tests", "cpp", "cblas_dlopen")
+    r = subprocess.run([exe, CBLAS_LIB], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "cblas dlopen ok" in r.stdout, r.stdout + r.stderr
+
+
+def _tile(dtype, M, N, K):
+    out = (ctypes.c_int * 4)()
+    assert _lib.lib().jules_hip_gemm_tile(dtype, M, N, K, out) == OK
+    return tuple(out)
+
+
+def test_gemm_tile_table():
+    """The launch table: C1 runs the row kernel with 2 rows per wave, the
+    reference's published shape [64,784]x[784,256] 1 row per wave, large fp32
+    GEMMs 64x64 tiles, C3 the bf16 LDS-DMA kernel, ragged bf16 the
+    register-staged one."""
+    assert _tile(0, 512, 512, 512) == (1, 8, 64, 512)
+    assert _tile(0, 64, 256, 784) == (0, 4, 64, 784)
+    assert _tile(0, 67, 80, 45) == (0, 4, 64, 48)
+    assert _tile(0, 512, 512, 4096) == (2, 32, 32, 32)        # K beyond the row kernel's LDS
+    assert _tile(0, 4096, 4096, 4096) == (3, 64, 64, 32)
+    assert _tile(0, 1024, 2048, 64) == (3, 64, 64, 32)        # 512 tiles of 64x64
+    assert _tile(0, 1024, 1040, 64) == (2, 32, 32, 32)        # 272 tiles of 64x64
+    assert _tile(1, 4096, 4096, 4096) == (4, 256, 256, 32)
+    assert _tile(1, 4104, 4096, 4096) == (5, 256, 256, 64)
+    out = (ctypes.c_int * 4)()
+    assert _lib.lib().jules_hip_gemm_tile(2, 4, 4, 4, out) == DTYPE
+    assert _lib.lib().jules_hip_gemm_tile(0, -1, 4, 4, out) == SHAPE
+    assert _lib.lib().jules_hip_gemm_tile(0, 4, 4, 4, None) == NULL
+
+
+@pytest.mark.parametrize("args,status", [
+    ((2, 0, 4, 4, 4, 1.0, P, 4, P, 4, 0.0, P, 4, None), ARG),      # transA not 0/1
+    ((0, 0, -1, 4, 4, 1.0, P, 4, P, 4, 0.0, P, 4, None), SHAPE),
+    ((0, 0, 4, 4, 4, 1.0, P, 3, P, 4, 0.0, P, 4, None), SHAPE),    # lda < K
+    ((1, 0, 5, 4, 4, 1.0, P, 4, P, 4, 0.0, P, 4, None), SHAPE),    # transA: lda < M
+    ((0, 1, 4, 5, 4, 1.0, P, 4, P, 3, 0.0, P, 5, None), SHAPE),    # transB: ldb < K
+    ((0, 0, 4, 4, 4, 1.0, P, 4, P, 4, 0.0, P, 3, None), SHAPE),    # ldc < N
+    ((0, 0, 4, 4, 4, 1.0, None, 4, P, 4, 0.0, P, 4, None), NULL),
+    ((0, 0, 4, 4, 4, 1.0, P, 4, P, 4, 0.0, None, 4, None), NULL),
+    ((0, 0, 4, 4, 4, 1.0, P + 2, 4, P, 4, 0.0, P, 4, None), ALIGN),
+    ((0, 0, 0, 4, 4, 1.0, None, 4, None, 4, 0.0, None, 4, None), OK),   # M = 0
+])
+def test_sgemm_validation(args, status):
+    assert _lib.lib().jules_hip_sgemm(*args) == status

@@ -194,17 +194,20 @@ def test_int8_bit_exact(dev, M, N, K):
 
 @pytest.mark.parametrize("M", [2, 40])
 def test_int8_extreme_sums(dev, M):
-    """K = 131072 (the largest K the entry point accepts) with every product
-    127 * -128: |sum| = 2,130,706,432, just inside int32; the split-K partials
-    and their atomic combination stay exact."""
+    """The largest |sum| the entry point can meet: every product (-128)*(-128)
+    = 2^14 at K = 131056 (the largest multiple of 16 within the K <= 131071
+    limit) sums to 2,147,221,504, just inside int32, and a column of
+    127 * -128 products to -2,130,444,288; the split-K partials and their
+    combination stay exact."""
     case(f"matmulInt8 extreme sums M={M}")
-    K, N = 131072, 16
-    A = np.full((M, K), 127, np.int8)
+    K, N = 131056, 16
+    A = np.full((M, K), -128, np.int8)
     B = np.full((K, N), -128, np.int8)
     B[:, 3] = 127
     y = to_np(ops.matmul_int8(to_dev(A, torch.int8, dev), to_dev(B, torch.int8, dev), 1.0, 1.0))
     np.testing.assert_array_equal(y, po.matmul_int8(A, B, 1.0, 1.0))
-    assert y[0, 0] == np.float32(-127 * 128 * K) and y[0, 3] == np.float32(127 * 127 * K)
+    assert y[0, 0] == np.float32(128 * 128 * K) and y[0, 3] == np.float32(-128 * 127 * K)
+    assert 128 * 128 * K < 2**31 and 128 * 128 * (K + 16) >= 2**31
 
 
 def test_int8_decode_two_streams(dev):
@@ -297,3 +300,32 @@ def test_w8a8_registry(dev):
                                       to_dev(bias, torch.float32, dev)], [c])
     assert st == 0, _lib.lib().jules_hip_last_error()
     np.testing.assert_array_equal(to_np(c), po.w8a8(A, B, sa, sb, bias))
+
+
+def test_w8a16_registry_two_streams(dev):
+    """The registry's W8A16 entry holds its split-K workspace per (device,
+    stream): calls alternating on two streams, with inputs of two sizes (each
+    stream's workspace grows once), give the bits of the typed entry point
+    with a caller workspace."""
+    case("registry matmulW8A16BiasSilu on two streams")
+    ins = []
+    for i, (M, N, K) in enumerate([(8, 2048, 4096), (16, 4096, 8192)]):
+        x, W, scale, bias = I.w8a16_inputs(M, N, K, seed=30 + i)
+        t = [to_dev(x, torch.bfloat16, dev), to_dev(W, torch.int8, dev),
+             to_dev(scale, torch.float32, dev), to_dev(bias, torch.float32, dev)]
+        ref = ops.w8a16_gemm(*t[:3], bias=t[3], act="silu")
+        ins.append((t, ref, (M, N)))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    outs = []
+    for rep in range(6):
+        for si, st in enumerate(streams):
+            t, ref, (M, N) = ins[(rep + si) % 2]
+            with torch.cuda.stream(st):
+                y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+                assert registry_call("matmulW8A16BiasSilu", t, [y]) == 0, \
+                    _lib.lib().jules_hip_last_error()
+                outs.append((y, ref))
+    torch.cuda.synchronize()
+    for y, ref in outs:
+        assert torch.equal(y, ref)
