@@ -214,6 +214,27 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W,
                                   void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* ---- W8A16 without allocation ------------------------------------------------
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The same computation, kernels and bits as
+ * jules_hip_w8a16_gemm_bias_act, with the split-K workspace taken from a
+ * library-held static device array instead of an argument; the call
+ * allocates nothing (no hipMalloc, hipFree or allocating library routine).
+ * Limit: the workspace of the shape must fit the array,
+ * jules_hip_w8a16_noalloc_max_bytes() bytes (8 MiB + 4 KiB: N <= 16384 at
+ * any K); larger shapes return JH_ERR_WORKSPACE.  Each GPU holds one such
+ * array for the life of the process and every call on that GPU shares it, so
+ * calls that overlap in time on one GPU (different streams, or threads
+ * without ordering) race and give wrong results; calls ordered on one stream
+ * are safe.  The array needs no clearing between calls (the reduction's
+ * flags are tagged with a per-call value).
+ */
+size_t jules_hip_w8a16_noalloc_max_bytes(void);
+int jules_hip_w8a16_gemm_bias_act_noalloc(int act, const void* x, const int8_t* W,
+                                          const float* scale, const float* bias,
+                                          void* y, int M, int N, int K, void* stream);
+
 /* ---- int8 x int8 GEMM (matmulInt8 semantics) -------------------------------
  * C[i,j] = float(sum_k A[i,k]*B[k,j]) * (scale_A*scale_B) [+ bias[j]]
  * Replaces matmulInt8(A,B,C,M,N,K,scale_A,scale_B,bias,arena) with the

@@ -247,20 +247,34 @@ size_t jules_hip_w8a16_workspace_size(int M, int N, int K) {
     return jh::w8a16_workspace_size(M, N, K);
 }
 
+// argument checks shared by the two W8A16 entry points; *done is set when
+// there is nothing to compute (M = 0 or N = 0)
+static int w8a16_check(const char* who, int act, const void* x, const int8_t* W, const float* scale,
+                       const float* bias, const void* y, int M, int N, int K, bool* done) {
+    *done = false;
+    if (!valid_act(act)) return fail(JH_ERR_ACT, "%s: activation code %d", who, act);
+    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "%s: M=%d N=%d K=%d", who, M, N, K);
+    if (M == 0 || N == 0) {
+        *done = true;
+        return JH_OK;
+    }
+    if (M > 16 || N % 16 || K % 8 || K == 0)
+        return fail(JH_ERR_UNSUPPORTED, "%s: needs 1<=M<=16, N%%16==0, K%%8==0, K>0 (got %d %d %d)",
+                    who, M, N, K);
+    if ((int64_t)K * N > kMaxElems) return fail(JH_ERR_SHAPE, "%s: too large", who);
+    if (!x || !W || !scale || !y) return fail(JH_ERR_NULL, "%s: null x, W, scale or y", who);
+    if (!aligned(W, 16) || !aligned(x, 16) || !aligned(y, 8) || !aligned(scale, 4) ||
+        !aligned(bias, 4))
+        return fail(JH_ERR_ALIGN, "%s: W, x 16-byte, y 8-byte, scale/bias 4-byte alignment", who);
+    return JH_OK;
+}
+
 int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W, const float* scale,
                                   const float* bias, void* y, int M, int N, int K,
                                   void* workspace, size_t workspace_bytes, void* stream) {
-    if (!valid_act(act)) return fail(JH_ERR_ACT, "w8a16: activation code %d", act);
-    if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "w8a16: M=%d N=%d K=%d", M, N, K);
-    if (M == 0 || N == 0) return JH_OK;
-    if (M > 16 || N % 16 || K % 8 || K == 0)
-        return fail(JH_ERR_UNSUPPORTED, "w8a16: needs 1<=M<=16, N%%16==0, K%%8==0, K>0 (got %d %d %d)",
-                    M, N, K);
-    if ((int64_t)K * N > kMaxElems) return fail(JH_ERR_SHAPE, "w8a16: too large");
-    if (!x || !W || !scale || !y) return fail(JH_ERR_NULL, "w8a16: null x, W, scale or y");
-    if (!aligned(W, 16) || !aligned(x, 16) || !aligned(y, 8) || !aligned(scale, 4) ||
-        !aligned(bias, 4))
-        return fail(JH_ERR_ALIGN, "w8a16: W, x 16-byte, y 8-byte, scale/bias 4-byte alignment");
+    bool done = false;
+    const int st = w8a16_check("w8a16", act, x, W, scale, bias, y, M, N, K, &done);
+    if (st != JH_OK || done) return st;
     const size_t need = jh::w8a16_workspace_size(M, N, K);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(JH_ERR_WORKSPACE, "w8a16: workspace %zu bytes, need %zu", workspace_bytes, need);
@@ -269,6 +283,29 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W, const
                                       static_cast<uint16_t*>(y), M, N, K, workspace,
                                       static_cast<hipStream_t>(stream)),
                      "w8a16 launch");
+}
+
+size_t jules_hip_w8a16_noalloc_max_bytes(void) { return jh::static_scratch_bytes(); }
+
+int jules_hip_w8a16_gemm_bias_act_noalloc(int act, const void* x, const int8_t* W,
+                                          const float* scale, const float* bias, void* y, int M,
+                                          int N, int K, void* stream) {
+    bool done = false;
+    const int st = w8a16_check("w8a16 noalloc", act, x, W, scale, bias, y, M, N, K, &done);
+    if (st != JH_OK || done) return st;
+    const size_t need = jh::w8a16_workspace_size(M, N, K);
+    if (need > jh::static_scratch_bytes())
+        return fail(JH_ERR_WORKSPACE,
+                    "w8a16 noalloc: M=%d N=%d K=%d needs %zu bytes of scratch, the library's "
+                    "static scratch holds %zu (N <= 16384 fits at any K)",
+                    M, N, K, need, jh::static_scratch_bytes());
+    void* ws = nullptr;
+    const int hst = check_hip(jh::static_scratch(&ws), "w8a16 noalloc: scratch address");
+    if (hst != JH_OK) return hst;
+    return check_hip(jh::launch_w8a16(act, static_cast<const uint16_t*>(x), W, scale, bias,
+                                      static_cast<uint16_t*>(y), M, N, K, ws,
+                                      static_cast<hipStream_t>(stream)),
+                     "w8a16 noalloc launch");
 }
 
 int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,

@@ -105,5 +105,10 @@ hipError_t launch_flash_bwd_padded(int dtype, int causal, float scale, const voi
 // device memory of `need` bytes for entry points without a workspace
 // argument: one buffer per (device, stream), kept for the process
 hipError_t stream_workspace(size_t need, hipStream_t s, void** ws);
+// the library's static device scratch (scratch.hip): its size, and the
+// device address of the current device's copy (looked up once per device;
+// allocates nothing)
+size_t static_scratch_bytes();
+hipError_t static_scratch(void** ptr);
 
 }  // namespace jh

@@ -336,3 +336,19 @@ def test_gemm_tile_table():
 ])
 def test_sgemm_validation(args, status):
     assert _lib.lib().jules_hip_sgemm(*args) == status
+
+
+def test_w8a16_noalloc_validation():
+    """The no-allocation W8A16 entry point checks its arguments like the
+    workspace one and rejects shapes whose workspace exceeds the static
+    scratch (65 column tiles x 8 splits here) before touching the device."""
+    L = _lib.lib()
+    f = L.jules_hip_w8a16_gemm_bias_act_noalloc
+    assert L.jules_hip_w8a16_noalloc_max_bytes() == (8 << 20) + 4096
+    assert f(9, P, P, P, None, P, 8, 64, 64, None) == ACT
+    assert f(5, P, P, P, None, P, 17, 64, 64, None) == UNSUP
+    assert f(5, None, P, P, None, P, 8, 64, 64, None) == NULL
+    assert f(5, P, P + 4, P, None, P, 8, 64, 64, None) == ALIGN
+    assert f(5, P, P, P, None, P, 8, 16640, 8192, None) == WS
+    assert b"static scratch" in L.jules_hip_last_error()
+    assert f(5, None, None, None, None, None, 0, 64, 64, None) == OK
