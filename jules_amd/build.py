@@ -8,6 +8,7 @@ and linked into jules_amd/libjules_hip.so.  Flags:
 """
 import concurrent.futures as cf
 import os
+import re
 import subprocess
 import sys
 
@@ -31,18 +32,46 @@ SOURCES = ["gemm_f32.hip", "gemm_bf16.hip", "flash_fwd.hip", "flash_bwd.hip", "f
            "pjrt.cpp"]
 
 
+def _scratch_kernels(stderr):
+    """Kernels whose resource-usage remark reports scratch (register spills or
+    private arrays): [(name, bytes per lane)]."""
+    found, name = [], None
+    for line in stderr.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0:
+            found.append((name, int(m.group(1))))
+    return found
+
+
 def _compile(src, verbose):
     path = os.path.join(CSRC, src)
     obj = os.path.join(OBJDIR, src + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [HIPCC, *COMMON, *DEVICE, *lang, "-c", path, "-o", obj]
+    remarks = ["-Rpass-analysis=kernel-resource-usage"] if src.endswith(".hip") else []
+    cmd = [HIPCC, *COMMON, *DEVICE, *remarks, *lang, "-c", path, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
-    if verbose and r.stderr.strip():
-        print(r.stderr, file=sys.stderr)
+    # Several kernels issue loads from inline asm and wait for them with
+    # explicit counters, so each destination register must stay untouched
+    # until its wait.  A kernel that spills breaks that: the compiler may
+    # store and reuse such a register while the load is in flight, and the
+    # late data then overwrites whatever it holds (an address, for example).
+    # No kernel of the library may use scratch.
+    spills = _scratch_kernels(r.stderr)
+    if spills:
+        raise RuntimeError(f"{src}: kernels use scratch (register spills), which the "
+                           f"asm-issued loads cannot tolerate: {spills}")
+    if verbose:
+        err = "\n".join(l for l in r.stderr.splitlines() if "kernel-resource-usage" not in l)
+        if err.strip():
+            print(err, file=sys.stderr)
     return obj
 
 

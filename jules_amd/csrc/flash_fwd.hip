@@ -86,8 +86,10 @@ __device__ __forceinline__ void block_coords(int BH, int nq, int bq, int* bh, in
 // K and V tiles of 64 keys go HBM -> LDS by the LDS DMA path
 // (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16 * lane)
 // through a ring of 4 stages; tile t lives in stage t % 4.  K_t is read in
-// phases 2t and 2t+1, V_t in phases 2t+2 and 2t+3, so tile t+4 is copied in
-// phase 2t+4 (all 8 waves share the copy) and has until phase 2t+8 to land.
+// phases 2t and 2t+1, V_t in phases 2t+2 and 2t+3, so the K half of tile
+// t+4 is copied in phase 2t+4 and its V half in phase 2t+5 (all 8 waves
+// share the copies; splitting them spreads their LDS writes over both
+// phases), and the tile has until phase 2t+8 to land.
 // Each lane's source address is permuted so the data lands in the swizzled
 // layouts below (LDS: 64 banks of 4 bytes; a ds_read_b128 serves 16 lanes per
 // clock, a ds_read_b64_tr_b16 32 lanes).  Both tiles are row-major [key][d],
@@ -246,7 +248,7 @@ __device__ __forceinline__ void flash_bf16_body(
     using C = Bf16Cfg<D>;
     constexpr int BKV = C::BKV;
     constexpr float kLazy = 8.0f;
-    constexpr int LA = 7;                       // MFMAs whose LDS reads are in flight
+    constexpr int LA = 8;                       // MFMAs whose LDS reads are in flight (at most 15 reads)
     constexpr int KR = LA + 2, VR = LA + 2;     // K / V fragment ring sizes
     constexpr int PIECES = 2 * C::SEGW;         // copy instructions per wave per tile
     __shared__ __attribute__((aligned(1024))) uint8_t sm[C::NSTAGE * C::STAGE];
@@ -285,9 +287,10 @@ __device__ __forceinline__ void flash_bf16_body(
     // ---- copy piece p of tile t: p < SEGW a K segment, else a V segment;
     // wave w moves segments w, w+8, ... of each operand tile ----
     const uint32_t sm0 = (uint32_t)(uintptr_t)sm;
-    auto dma_tile = [&](int t) {
+    auto dma_part = [&](int t, int p0, int p1) {
 #pragma unroll
         for (int p = 0; p < PIECES; ++p) {
+            if (p < p0 || p >= p1) continue;
             const int i = p % C::SEGW;
             const int seg = i * NW2 + wave;
             const int r = seg * C::RPS + lane / C::UNITS;  // row within the tile
@@ -302,6 +305,7 @@ __device__ __forceinline__ void flash_bf16_body(
                                                  (lds_void*)(dst + C::TILE), 16, 0, 0);
         }
     };
+    auto dma_tile = [&](int t) { dma_part(t, 0, PIECES); };
 
     // ---- per-lane LDS offsets within a stage (recomputed per phase, which
     // costs a few VALU ops in the MFMA phase but no registers across phases) ----
@@ -336,6 +340,8 @@ __device__ __forceinline__ void flash_bf16_body(
     auto mfma_phase = [&](int j, auto do_s_tag, auto do_pv_tag) {
         constexpr bool DO_S = decltype(do_s_tag)::value;
         constexpr bool DO_PV = decltype(do_pv_tag)::value;
+        // the MFMA wave's issue goes first when both waves of a SIMD are ready
+        __builtin_amdgcn_s_setprio(1);
         using Q_ = MfmaSeq<DO_S, DO_PV, C::NS, C::NPV>;
         constexpr int NM = Q_::NM;
         constexpr int TOT = Q_::reads_upto(NM - 1);
@@ -392,20 +398,23 @@ __device__ __forceinline__ void flash_bf16_body(
             constexpr int nxt = Q_::reads_upto(m + LA < NM - 1 ? m + LA : NM - 1);
             static_for<issued, nxt>(issue_read);
         });
+        __builtin_amdgcn_s_setprio(0);
     };
 
     // ---- SOFTMAX(j) ----
     auto softmax_phase = [&](int j) {
         const int k0 = j * BKV;
         if (k0 + BKV > S || (CAUSAL && k0 + BKV - 1 > qw0)) {
-            // keys past S and (causal) keys after this lane's query -> -inf
+            // keys past S and (causal) keys after this lane's query -> -inf.
+            // Element (h, e) holds key k0 + 4g + off with off = 32h + 8(e/4) +
+            // e%4 a constant, so one compare against a per-lane limit masks it.
+            int lim = S - 1 - k0 - 4 * g;
+            if (CAUSAL) lim = min(lim, qrow - k0 - 4 * g);
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int key = k0 + h * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-                    if (key >= S || (CAUSAL && key > qrow)) sc[h][e] = kNegInf;
-                }
+                for (int e = 0; e < 16; ++e)
+                    if (h * 32 + 8 * (e >> 2) + (e & 3) > lim) sc[h][e] = kNegInf;
         }
         float mx = kNegInf;
 #pragma unroll
@@ -458,50 +467,65 @@ __device__ __forceinline__ void flash_bf16_body(
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
     // Phases 0 .. 2 n_kv + 1, each closed by a barrier of all 8 waves.
-    // Copies of tile u+2 are issued in phase 2u (into the stage tile u-2 left,
-    // last read in phase 2u-1).  Before phase 2u, tile u must have landed:
-    // the copies issued after it are those of tile u+1.
-    auto copy_ahead = [&](int u) {
-        if (u + 2 < n_kv) dma_tile(u + 2);
+    // Tile u+2 is copied into the stage tile u-2 left (last read in phase
+    // 2u-1): its K half in phase 2u, its V half in phase 2u+1, which spreads
+    // the copies' LDS writes over both phases.  Before phase 2u, tile u must
+    // have landed: the copies issued after it are those of tile u+1.
+    auto copy_k = [&](int u) {
+        if (u + 2 < n_kv) dma_part(u + 2, 0, C::SEGW);
+    };
+    auto copy_v = [&](int u) {
+        if (u + 2 < n_kv) dma_part(u + 2, C::SEGW, PIECES);
     };
     auto land = [&](int u) {
         if (u < n_kv) vm_wait(u + 1 < n_kv ? PIECES : 0);
     };
+    // Causal: key tile t is needed by this wave only if its first key is at
+    // or before the wave's last query.  A wave skips the softmax and the S
+    // products of tiles it does not need (every wave still copies and meets
+    // every barrier).  MFMA(j) also carries PV_{j-1}, so it runs while tile
+    // j-1 is needed; for the first unneeded tile j its S_j is computed and
+    // left unused, which keeps a single MFMA-phase shape in the loop.
+    auto need = [&](int t) { return !CAUSAL || t * BKV <= qw0 + 31; };
     if (grp == 0) {
-        copy_ahead(0);
+        copy_k(0);
         mfma_phase(0, yes{}, no{});
         bare_barrier();  // phase 0
+        copy_v(0);
         softmax_phase(0);
         land(1);
         bare_barrier();  // phase 1
         for (int j = 1; j < n_kv; ++j) {
-            copy_ahead(j);
-            mfma_phase(j, yes{}, yes{});
+            copy_k(j);
+            if (need(j - 1)) mfma_phase(j, yes{}, yes{});
             bare_barrier();  // phase 2j
-            softmax_phase(j);
+            copy_v(j);
+            if (need(j)) softmax_phase(j);
             land(j + 1);
             bare_barrier();  // phase 2j+1
         }
-        mfma_phase(n_kv, no{}, yes{});
+        if (need(n_kv - 1)) mfma_phase(n_kv, no{}, yes{});
         bare_barrier();  // phase 2 n_kv
         bare_barrier();  // phase 2 n_kv + 1
     } else {
-        copy_ahead(0);
+        copy_k(0);
         bare_barrier();  // phase 0
+        copy_v(0);
         mfma_phase(0, yes{}, no{});
         land(1);
         bare_barrier();  // phase 1
         for (int j = 1; j < n_kv; ++j) {
-            copy_ahead(j);
-            softmax_phase(j - 1);
+            copy_k(j);
+            if (need(j - 1)) softmax_phase(j - 1);
             bare_barrier();  // phase 2j
-            mfma_phase(j, yes{}, yes{});
+            copy_v(j);
+            if (need(j - 1)) mfma_phase(j, yes{}, yes{});
             land(j + 1);
             bare_barrier();  // phase 2j+1
         }
-        softmax_phase(n_kv - 1);
+        if (need(n_kv - 1)) softmax_phase(n_kv - 1);
         bare_barrier();  // phase 2 n_kv
-        mfma_phase(n_kv, no{}, yes{});
+        if (need(n_kv - 1)) mfma_phase(n_kv, no{}, yes{});
         bare_barrier();  // phase 2 n_kv + 1
     }
 
