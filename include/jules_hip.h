@@ -202,7 +202,9 @@ int jules_hip_flash_attn_bwd(int dtype, int causal, float scale,
  * 16 KiB with KS <= 8, then one 8-byte flag per tile and split; one launch
  * does the split-K reduction); it needs no initialisation and is
  * overwritten by every call.  Calls that overlap in time need separate
- * workspaces.
+ * workspaces.  The flags are tagged with a value chosen when the call is
+ * made, so a launch captured in a HIP graph must not be replayed; graph
+ * callers use jules_hip_w8a16_gemm_bias_act_noalloc.
  * No reference counterpart: the reference's int8 kernel (matmulInt8,
  * FusedKernels.h:867) is W8A8 with one scalar scale; routed name
  * "matmulW8A16BiasSilu" is new.
@@ -227,8 +229,11 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W,
  * array for the life of the process and every call on that GPU shares it, so
  * calls that overlap in time on one GPU (different streams, or threads
  * without ordering) race and give wrong results; calls ordered on one stream
- * are safe.  The array needs no clearing between calls (the reduction's
- * flags are tagged with a per-call value).
+ * are safe.  The split-K reduction finds each column tile's last workgroup
+ * with an arrival counter in the array that the last workgroup resets, so
+ * the launch carries no per-call value: the call may be captured in a HIP
+ * graph and replayed (the workspace entry point cannot: its completion flags
+ * are tagged with a value chosen at launch, which capture would freeze).
  */
 size_t jules_hip_w8a16_noalloc_max_bytes(void);
 int jules_hip_w8a16_gemm_bias_act_noalloc(int act, const void* x, const int8_t* W,

@@ -293,18 +293,22 @@ int jules_hip_w8a16_gemm_bias_act_noalloc(int act, const void* x, const int8_t* 
     bool done = false;
     const int st = w8a16_check("w8a16 noalloc", act, x, W, scale, bias, y, M, N, K, &done);
     if (st != JH_OK || done) return st;
-    const size_t need = jh::w8a16_workspace_size(M, N, K);
-    if (need > jh::static_scratch_bytes())
+    const size_t need = jh::w8a16_partials_size(M, N, K);
+    if (need > jh::static_scratch_partial_bytes() || N > 16384)
         return fail(JH_ERR_WORKSPACE,
-                    "w8a16 noalloc: M=%d N=%d K=%d needs %zu bytes of scratch, the library's "
+                    "w8a16 noalloc: M=%d N=%d K=%d needs %zu bytes of partials, the library's "
                     "static scratch holds %zu (N <= 16384 fits at any K)",
-                    M, N, K, need, jh::static_scratch_bytes());
+                    M, N, K, need, jh::static_scratch_partial_bytes());
     void* ws = nullptr;
     const int hst = check_hip(jh::static_scratch(&ws), "w8a16 noalloc: scratch address");
     if (hst != JH_OK) return hst;
-    return check_hip(jh::launch_w8a16(act, static_cast<const uint16_t*>(x), W, scale, bias,
-                                      static_cast<uint16_t*>(y), M, N, K, ws,
-                                      static_cast<hipStream_t>(stream)),
+    // partials first, the per-tile counters at a fixed offset after them
+    char* base = static_cast<char*>(ws);
+    return check_hip(jh::launch_w8a16_counters(
+                         act, static_cast<const uint16_t*>(x), W, scale, bias,
+                         static_cast<uint16_t*>(y), M, N, K, reinterpret_cast<float*>(base),
+                         reinterpret_cast<uint32_t*>(base + jh::static_scratch_partial_bytes()),
+                         static_cast<hipStream_t>(stream)),
                      "w8a16 noalloc launch");
 }
 

@@ -46,6 +46,13 @@ hipError_t launch_int8_decode(const int8_t* A, const int8_t* B, float* C, int M,
 hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float* scale,
                         const float* bias, uint16_t* y, int M, int N, int K, void* ws,
                         hipStream_t s);
+// the same computation with the last workgroup of each column tile found by
+// an arrival counter (counters: one uint32 per 256-column tile, zero before
+// the call, left at zero); partials: w8a16_partials_size(M, N, K) bytes
+size_t w8a16_partials_size(int M, int N, int K);
+hipError_t launch_w8a16_counters(int act, const uint16_t* x, const int8_t* W, const float* scale,
+                                 const float* bias, uint16_t* y, int M, int N, int K,
+                                 float* partials, uint32_t* counters, hipStream_t s);
 hipError_t launch_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                               float scale_a, float scale_b, const float* bias, hipStream_t s);
 hipError_t launch_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
@@ -109,6 +116,7 @@ hipError_t stream_workspace(size_t need, hipStream_t s, void** ws);
 // device address of the current device's copy (looked up once per device;
 // allocates nothing)
 size_t static_scratch_bytes();
+size_t static_scratch_partial_bytes();  // the partial-tile part; the counters follow it
 hipError_t static_scratch(void** ptr);
 
 }  // namespace jh

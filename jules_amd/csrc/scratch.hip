@@ -12,8 +12,10 @@
 #include "launch.hpp"
 
 // 8 MiB of split-K partials (8 splits x 64 column tiles of 16 KiB: N up to
-// 16384 at any K) plus one 8-byte flag per (tile, split)
-static constexpr size_t kScratchBytes = (size_t(8) << 20) + 64 * 8 * 8;
+// 16384 at any K), then 4 KiB holding the per-tile arrival counters (zero at
+// load; every call leaves them at zero)
+static constexpr size_t kPartialBytes = size_t(8) << 20;
+static constexpr size_t kScratchBytes = kPartialBytes + 4096;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace jh {
@@ -24,6 +26,7 @@ void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device
 }  // namespace
 
 size_t static_scratch_bytes() { return kScratchBytes; }
+size_t static_scratch_partial_bytes() { return kPartialBytes; }
 
 hipError_t static_scratch(void** ptr) {
     int dev = 0;

@@ -83,12 +83,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* partials, int
                                              0, valid ? PART_FLOATS * 4 : 0, 0x00020000);
 }
 
-template <int ACT>
+// COUNTER selects how the last workgroup of a column tile is found: per-call
+// flags (flags, call_id; the workspace needs no initialisation) or one
+// arrival counter per tile (counters; zero before the call and reset to zero
+// by the tile's last workgroup, so the launch arguments never change from
+// call to call and a captured graph can replay the launch).
+template <int ACT, bool COUNTER>
 __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ W, int M, int N, int K, int KS,
     int steps, float* __restrict__ partials, const float* __restrict__ scale,
     const float* __restrict__ bias, uint16_t* __restrict__ y, uint64_t* __restrict__ flags,
-    uint64_t call_id) {
+    uint64_t call_id, uint32_t* __restrict__ counters) {
     __shared__ f32x4_t red[WAVES * 16 * 64];  // 128 KiB: [wave][j][lane]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -209,6 +214,11 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     // they write the same bits (same partials, summed in split order).
     // call_id is new for every call, so flags from earlier calls or
     // uninitialised workspace never match.
+    // Counter protocol (COUNTER): after its partial stores complete, wave 0
+    // adds 1 to counters[tile] (agent-scope atomic with return); the
+    // workgroup that receives KS-1 is the tile's last arrival, resets the
+    // counter to 0 for the next call and reduces.  Exactly one workgroup
+    // reduces.
     const int tiles = gridDim.x;
     const int lanes_live = 16 * ((M + 3) / 4);  // lanes holding rows < M
     const bool live = lane < lanes_live;
@@ -224,7 +234,15 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's partial stores are done
     __shared__ int last;
     lds_barrier();                        // ... and every wave's
-    if (wave == 0) {
+    if constexpr (COUNTER) {
+        if (wave == 0 && lane == 0) {
+            const uint32_t old =
+                __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool is_last = old == (uint32_t)(KS - 1);
+            if (is_last) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = is_last;
+        }
+    } else if (wave == 0) {
         uint64_t* tf = flags + (int64_t)tile * KS;
         if (lane == 0) __hip_atomic_store(tf + split, call_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -529,8 +547,30 @@ hipError_t launch_w8a16(int act, const uint16_t* x, const int8_t* W, const float
     const uint64_t id = next_call_id();
     hipError_t e = hipSuccess;
     JH_DISPATCH_ACT(act, ACT, {
-        hipLaunchKernelGGL(w8a16_splitk_kernel<ACT>, dim3(tiles, p.ks), dim3(THREADS), 0, s, x, W, M,
-                           N, K, p.ks, p.steps, partials, scale, bias, y, flags, id);
+        hipLaunchKernelGGL((w8a16_splitk_kernel<ACT, false>), dim3(tiles, p.ks), dim3(THREADS), 0, s,
+                           x, W, M, N, K, p.ks, p.steps, partials, scale, bias, y, flags, id,
+                           nullptr);
+        e = hipGetLastError();
+    });
+    return e;
+}
+
+size_t w8a16_partials_size(int M, int N, int K) {
+    (void)M;
+    const Plan p = plan(K);
+    return (size_t)((N + COLS - 1) / COLS) * p.ks * PART_FLOATS * sizeof(float);
+}
+
+hipError_t launch_w8a16_counters(int act, const uint16_t* x, const int8_t* W, const float* scale,
+                                 const float* bias, uint16_t* y, int M, int N, int K,
+                                 float* partials, uint32_t* counters, hipStream_t s) {
+    const Plan p = plan(K);
+    const int tiles = (N + COLS - 1) / COLS;
+    hipError_t e = hipSuccess;
+    JH_DISPATCH_ACT(act, ACT, {
+        hipLaunchKernelGGL((w8a16_splitk_kernel<ACT, true>), dim3(tiles, p.ks), dim3(THREADS), 0, s,
+                           x, W, M, N, K, p.ks, p.steps, partials, scale, bias, y, nullptr,
+                           uint64_t(0), counters);
         e = hipGetLastError();
     });
     return e;

@@ -4,7 +4,8 @@ callers that cannot allocate): through the C ABI its output equals the bits of
 jules_hip_w8a16_gemm_bias_act with a caller workspace (same kernels, fixed
 reduction order) on consecutive calls whose sizes shrink, so the second call
 runs on the scratch the first one left behind; the largest shape that fits the
-static scratch works, and one column tile more is rejected before any launch."""
+static scratch works, and one column tile more is rejected before any launch;
+captured once in a HIP graph, the call replays correctly with new inputs."""
 import pytest
 import torch
 
@@ -67,3 +68,31 @@ def test_noalloc_size_limit(dev):
     y2 = torch.empty((M, N + 256), dtype=torch.bfloat16, device=dev)
     assert _noalloc(x, W2, s2, None, "silu", y2) == WORKSPACE
     assert b"static scratch" in L.jules_hip_last_error()
+
+
+def test_noalloc_graph_replay(dev):
+    """Callers under graph capture: the launch is captured once and replayed
+    with new activations copied in between (eager work and a synchronisation
+    between replays); every replay equals the eager workspace entry point on
+    the same inputs.  The kernel's launch arguments carry no per-call value
+    (its tiles' arrival counters are reset by their last workgroup), so a
+    replay cannot mistake an earlier replay's partial tiles for its own."""
+    M, N, K = 8, 4096, 4096
+    case(f"w8a16 noalloc captured in a graph {M}x{N}x{K}")
+    x, W, scale, bias = _operands(dev, M, N, K, 3)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    assert _noalloc(x, W, scale, bias, "silu", y) == OK  # eager first call
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = _noalloc(x, W, scale, bias, "silu", y)
+    assert st == OK, _lib.lib().jules_hip_last_error()
+    for i in range(4):
+        xi, _, _, _ = _operands(dev, M, N, K, 10 + i)
+        x.copy_(xi)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref = ops.w8a16_gemm(x, W, scale, bias, "silu")
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {i}"
