@@ -362,6 +362,18 @@ int jules_hip_mlp_forward_backward(const float* X, const float* W1, const float*
  */
 int jules_hip_mfma_ceiling(float* out, int workgroups, int iters, void* stream);
 
+/* ---- HBM read calibration ---------------------------------------------------
+ * No counterpart in the reference: the read rate a plain streaming read
+ * attains, the floor an HBM-bound kernel such as the W8A16 GEMM is compared
+ * with next to the published 8 TB/s.  Reads `bytes` (a multiple of 16) of
+ * `buf` once with 16-byte nontemporal loads, 8 in flight per lane, from
+ * `workgroups` x 256 lanes (256 workgroups measured fastest for 64 MiB);
+ * out: device uint32 [workgroups * 256], 4-byte aligned, receives values that
+ * only keep the loads live.  buf 16-byte aligned.
+ */
+int jules_hip_hbm_read_floor(const void* buf, int64_t bytes, uint32_t* out, int workgroups,
+                             void* stream);
+
 /* ---- kernel-name registry -------------------------------------------------
  * Resolves the names KernelRoutingPass emits (fusedMatmul{Relu,Sigmoid,Tanh,
  * Gelu}, fusedMatmulBias{Relu,Sigmoid,Tanh,Gelu}, fusedGelu, matmulInt8,

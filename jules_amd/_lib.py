@@ -56,6 +56,7 @@ SIGNATURES = {
     "jules_hip_matmul_w8a8": (_int, [_vp, _vp, _vp, _int, _int, _int, _vp, _vp, _vp, _vp]),
     "jules_hip_softmax": (_int, [_vp, _vp, _int, _int, _vp]),
     "jules_hip_mfma_ceiling": (_int, [_vp, _int, _int, _vp]),
+    "jules_hip_hbm_read_floor": (_int, [_vp, _i64, _vp, _int, _vp]),
     "jules_hip_layernorm": (_int, [_vp, _vp, _vp, _vp, _int, _int, _f32, _vp]),
     "jules_hip_cross_entropy_workspace_size": (_size, [_int]),
     "jules_hip_cross_entropy": (_int, [_vp, _vp, _vp, _vp, _int, _int, _vp, _size, _vp]),

@@ -386,6 +386,20 @@ int jules_hip_mfma_ceiling(float* out, int workgroups, int iters, void* stream) 
                      "mfma_ceiling");
 }
 
+int jules_hip_hbm_read_floor(const void* buf, int64_t bytes, uint32_t* out, int workgroups,
+                             void* stream) {
+    if (!buf || !out) return fail(JH_ERR_NULL, "hbm_read_floor: null buffer or out");
+    if (!aligned(buf, 16) || !aligned(out, 4))
+        return fail(JH_ERR_ALIGN, "hbm_read_floor: buf 16-byte, out 4-byte alignment");
+    if (bytes < 16 || bytes % 16 || bytes > (int64_t(1) << 40))
+        return fail(JH_ERR_SHAPE, "hbm_read_floor: bytes %lld (a multiple of 16, >= 16)",
+                    (long long)bytes);
+    if (workgroups < 1 || workgroups > 65535)
+        return fail(JH_ERR_SHAPE, "hbm_read_floor: workgroups %d (1..65535)", workgroups);
+    return check_hip(jh::launch_hbm_read(buf, bytes, out, workgroups, static_cast<hipStream_t>(stream)),
+                     "hbm_read_floor");
+}
+
 size_t jules_hip_cross_entropy_workspace_size(int M) {
     return M > 0 ? (size_t)M * sizeof(float) : sizeof(float);
 }

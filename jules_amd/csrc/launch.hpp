@@ -97,6 +97,10 @@ hipError_t launch_pj_reduce(const float* in, float* out, int64_t n_out, int64_t 
 
 // calibration: workgroups x 4 waves x 16*iters MFMAs on random operands
 hipError_t launch_mfma_ceiling(float* out, int workgroups, int iters, hipStream_t s);
+// calibration: a plain streaming read of `bytes` (a multiple of 16) by
+// `workgroups` x 256 lanes; out receives workgroups * 256 uint32
+hipError_t launch_hbm_read(const void* buf, int64_t bytes, uint32_t* out, int workgroups,
+                           hipStream_t s);
 
 
 // flash attention at head dims other than 64 and 128 (1 <= D <= 128): inputs

@@ -390,3 +390,19 @@ def mfma_ceiling(out, workgroups, iters):
     _on_device(out=out)
     check(lib().jules_hip_mfma_ceiling(_ptr(out), int(workgroups), int(iters), _stream(out)))
     return 32768.0 * 16 * iters * 4 * workgroups
+
+
+def hbm_read_floor(buf, out, workgroups=256):
+    """Launch the HBM read calibration (jules_hip_hbm_read_floor; no
+    counterpart in the reference) on torch's current stream: one streaming
+    read of `buf` (contiguous, a multiple of 16 bytes).  out: int32 GPU tensor
+    of workgroups * 256 elements.  Returns the bytes read."""
+    if not isinstance(buf, torch.Tensor) or not buf.is_contiguous():
+        raise ValueError("buf must be a contiguous tensor")
+    _need(out, "out", (torch.int32,))
+    if out.numel() < workgroups * 256:
+        raise ValueError("out must hold workgroups * 256 int32")
+    _on_device(buf=buf, out=out)
+    nbytes = buf.numel() * buf.element_size()
+    check(lib().jules_hip_hbm_read_floor(_ptr(buf), nbytes, _ptr(out), int(workgroups), _stream(buf)))
+    return nbytes

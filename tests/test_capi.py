@@ -352,3 +352,14 @@ def test_w8a16_noalloc_validation():
     assert f(5, P, P, P, None, P, 8, 16640, 8192, None) == WS
     assert b"static scratch" in L.jules_hip_last_error()
     assert f(5, None, None, None, None, None, 0, 64, 64, None) == OK
+
+
+def test_hbm_read_floor_validation():
+    L = _lib.lib()
+    f = L.jules_hip_hbm_read_floor
+    assert f(None, 1 << 20, P, 256, None) == NULL
+    assert f(P, 1 << 20, None, 256, None) == NULL
+    assert f(P + 8, 1 << 20, P, 256, None) == ALIGN
+    assert f(P, (1 << 20) + 8, P, 256, None) == SHAPE
+    assert f(P, 0, P, 256, None) == SHAPE
+    assert f(P, 1 << 20, P, 0, None) == SHAPE

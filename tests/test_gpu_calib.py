@@ -1,11 +1,13 @@
-"""GPU run of the MFMA calibration kernel (jules_hip_mfma_ceiling): it
-launches, its output is finite and deterministic (the operands are a fixed
-hash), and an odd workgroup count covers the output indexing."""
+"""GPU runs of the calibration kernels.  The MFMA ceiling
+(jules_hip_mfma_ceiling) launches, its output is finite and deterministic
+(the operands are a fixed hash), and an odd workgroup count covers the output
+indexing; the HBM read floor (jules_hip_hbm_read_floor) reads every chunk of
+its buffer exactly once."""
 import numpy as np
 import pytest
 import torch
 
-from jules_amd import _lib
+from jules_amd import _lib, ops
 from tests.helpers import case
 
 pytestmark = pytest.mark.gpu
@@ -25,3 +27,17 @@ def test_mfma_ceiling_runs(dev, workgroups, iters):
     assert st == 0
     torch.cuda.synchronize()
     assert np.array_equal(a, out.cpu().numpy())
+
+
+def test_hbm_read_floor_reads_every_chunk_once(dev):
+    """XOR over all lanes' results equals the XOR of every 4-byte word of the
+    buffer: each 16-byte chunk is read exactly once (grid-stride tail
+    included)."""
+    case("hbm read floor: every chunk read once")
+    n = (1 << 20) + 16 * 37  # not a multiple of the grid's stride
+    host = np.random.default_rng(3).integers(-2**31, 2**31 - 1, n // 4, dtype=np.int64).astype(np.int32)
+    buf = torch.from_numpy(host).to(dev)
+    out = torch.empty(256 * 256, dtype=torch.int32, device=dev)
+    assert ops.hbm_read_floor(buf, out, 256) == n
+    got = np.bitwise_xor.reduce(out.cpu().numpy())
+    assert got == np.bitwise_xor.reduce(host)
