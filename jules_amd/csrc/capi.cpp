@@ -49,6 +49,8 @@ constexpr int64_t kMaxElems = int64_t(1) << 40;
 // largest int8 GEMM depth whose int32 sums cannot overflow: every product
 // is at most (-128)*(-128) = 2^14, and 131071 * 2^14 < 2^31
 constexpr int kMaxInt8K = 131071;
+// W8A16 decode: x and one k-step of W are addressed with 32-bit buffer offsets
+constexpr int kMaxDecodeDim = 1 << 26;
 
 }  // namespace
 
@@ -258,9 +260,10 @@ static int w8a16_check(const char* who, int act, const void* x, const int8_t* W,
         *done = true;
         return JH_OK;
     }
-    if (M > 16 || N % 16 || K % 8 || K == 0)
-        return fail(JH_ERR_UNSUPPORTED, "%s: needs 1<=M<=16, N%%16==0, K%%8==0, K>0 (got %d %d %d)",
-                    who, M, N, K);
+    if (M > 16 || N % 16 || K % 8 || K == 0 || N > kMaxDecodeDim || K > kMaxDecodeDim)
+        return fail(JH_ERR_UNSUPPORTED,
+                    "%s: needs 1<=M<=16, N%%16==0, K%%8==0, 0<K<=2^26, N<=2^26 (got %d %d %d)", who, M,
+                    N, K);
     if ((int64_t)K * N > kMaxElems) return fail(JH_ERR_SHAPE, "%s: too large", who);
     if (!x || !W || !scale || !y) return fail(JH_ERR_NULL, "%s: null x, W, scale or y", who);
     if (!aligned(W, 16) || !aligned(x, 16) || !aligned(y, 8) || !aligned(scale, 4) ||

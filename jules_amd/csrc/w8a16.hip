@@ -40,7 +40,7 @@ constexpr int COLS = 256;       // columns per workgroup: 16 lanes x 16 columns
 constexpr int WAVES = 8;
 constexpr int THREADS = WAVES * 64;
 constexpr int KSTEP = 32;       // rows per MFMA k-step
-constexpr int GROUP = 2;        // k-steps whose loads are in flight together
+constexpr int DEPTH = 4;        // k-steps per wave in flight
 constexpr int MAX_KS = 8;       // most K splits (partials) per output
 // s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt unconstrained (gfx9 encoding)
 constexpr unsigned kWaitVm0 = 0x0F70;
@@ -52,10 +52,10 @@ struct Plan {
 
 inline Plan plan(int K) {
     const int total_steps = (K + KSTEP - 1) / KSTEP;
-    // aim for two groups of GROUP k-steps per wave (measured best at
-    // K = N = 8192: fewer splits starve the chip, more cost partial traffic);
-    // at most MAX_KS splits (larger K gives each wave more k-steps)
-    int ks = (total_steps + 2 * WAVES * GROUP - 1) / (2 * WAVES * GROUP);
+    // aim for DEPTH k-steps per wave, all in flight from the start (fewer
+    // splits starve the chip, more cost partial traffic); at most MAX_KS
+    // splits (larger K gives each wave more k-steps)
+    int ks = (total_steps + WAVES * DEPTH - 1) / (WAVES * DEPTH);
     if (ks > MAX_KS) ks = MAX_KS;
     if (ks < 1) ks = 1;
     const int per_split = (total_steps + ks - 1) / ks;
@@ -63,8 +63,13 @@ inline Plan plan(int K) {
     return {ks, steps};
 }
 
-// cache policy bits of buffer instructions: sc1 (coherent at agent scope)
+// cache policy bits of buffer instructions: nt (streaming), sc1 (coherent at
+// agent scope)
+constexpr int kNT = 2;
 constexpr int kSc1 = 16;
+// a buffer offset past every range used here (buffers hold < 2^31 bytes):
+// loads there return 0, stores are dropped
+constexpr uint32_t kOOB = 0x80000000u;
 constexpr int PART_FLOATS = 16 * 64 * 4;  // one (split, tile) partial: [j][lane] x 4 rows
 
 // Workgroup barrier that orders LDS accesses only: global loads and stores
@@ -96,7 +101,9 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     uint64_t call_id, uint32_t* __restrict__ counters) {
     __shared__ f32x4_t red[WAVES * 16 * 64];  // 128 KiB: [wave][j][lane]
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave index through readfirstlane: the compiler then knows it (and the
+    // per-step buffer resources built from it) to be wave-uniform
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tile = blockIdx.x, split = blockIdx.y;
     const int n0 = tile * COLS;
     const int lc = lane & 15, lg = lane >> 4;     // column chunk, k group
@@ -124,51 +131,65 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     const int s0 = split * per_split;
     const int s1 = min(total_steps, s0 + per_split);
 
-    for (int t0 = 0; t0 < steps; t0 += GROUP) {
-        u32x4_t wr[GROUP][8];
-        bf16x8_t xa[GROUP];
+    // Weight stream: DEPTH k-steps of every wave in flight (for the decode
+    // shape, all of them from the start), each converted as soon as its
+    // loads land while the later ones stream.  The loads are buffer loads,
+    // whose range check stands in for every bounds test: a k-step gets a
+    // buffer over its own rows (no bytes for a step past the split: all its
+    // loads return 0), a lane past N gets an out-of-range offset, and the x
+    // loads get one where the row is past M or the k-range past K.  So no
+    // loaded value passes through a select, and each is waited for only
+    // where it is converted.  A lane's offset within a step is fixed: row
+    // 8*lg + r, its 16 columns.
+    uint32_t wofs[8];
 #pragma unroll
-        for (int u = 0; u < GROUP; ++u) {
-            const int st = s0 + wave + WAVES * (t0 + u);
-            const bool live = (t0 + u < steps) && st < s1;
-            const int kb = st * KSTEP + 8 * lg;  // this lane's 8 rows
-            // Branch-free loads: an out-of-range lane reads element 0 and the
-            // value is dropped by a select, so the compiler can wait on each
-            // load separately (vmcnt) instead of draining all of them.
+    for (int r = 0; r < 8; ++r) wofs[r] = col_ok ? (uint32_t)(8 * lg + r) * (uint32_t)N + col0 : kOOB;
+    const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(x), 0, (uint32_t)M * (uint32_t)K * 2u, 0x00020000);
+
+    u32x4_t wr[DEPTH][8];
+    u32x4_t xr[DEPTH];
+    auto issue = [&](int t, int slot) {
+        const int st = s0 + wave + WAVES * t;
+        const bool live = t < steps && st < s1;
+        const int rows = live ? min(K - st * KSTEP, KSTEP) : 0;
+        const __amdgpu_buffer_rsrc_t wsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(W) + (live ? (int64_t)st * KSTEP * N : 0), 0, (uint32_t)rows * (uint32_t)N,
+            0x00020000);
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const bool ok = live && col_ok && kb + r < K;
-                const int64_t off = ok ? (int64_t)(kb + r) * N + col0 : 0;
-                const u32x4_t v =
-                    __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(W + off));
-                const u32x4_t z = {0u, 0u, 0u, 0u};
-                wr[u][r] = ok ? v : z;
-            }
-            // A operand: x[m = lane & 15][kb .. kb+7]
-            const bool xok = live && lc < M && kb < K;
-            const u32x4_t xv =
-                *reinterpret_cast<const u32x4_t*>(x + (xok ? (int64_t)lc * K + kb : 0));
-            const u32x4_t z = {0u, 0u, 0u, 0u};
-            xa[u] = __builtin_bit_cast(bf16x8_t, xok ? xv : z);
+        for (int r = 0; r < 8; ++r) wr[slot][r] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, wofs[r], 0, kNT);
+        // A operand: x[m = lane & 15][kb .. kb+7]
+        const int kb = st * KSTEP + 8 * lg;
+        const uint32_t xo = (live && lc < M && kb < K) ? (uint32_t)(lc * K + kb) * 2u : kOOB;
+        xr[slot] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, xo, 0, 0);
+    };
+    auto convert_mfma = [&](int slot) {
+        const bf16x8_t xa = __builtin_bit_cast(bf16x8_t, xr[slot]);
+        // column j of the 16: bytes j of the 8 rows -> 8 bf16 (k = kb..kb+7)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int dw = j >> 2, sh = 8 * (j & 3);
+            float f[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) f[r] = (float)(int8_t)(wr[slot][r][dw] >> sh);
+            u32x4_t b;
+            b[0] = pack_bf16x2(f[0], f[1]);
+            b[1] = pack_bf16x2(f[2], f[3]);
+            b[2] = pack_bf16x2(f[4], f[5]);
+            b[3] = pack_bf16x2(f[6], f[7]);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(bf16x8_t, b), acc[j], 0, 0, 0);
         }
+    };
+
 #pragma unroll
-        for (int u = 0; u < GROUP; ++u) {
-            if (t0 + u >= steps) break;
-            // column j of the 16: bytes j of the 8 rows -> 8 bf16 (k = kb..kb+7)
+    for (int d = 0; d < DEPTH; ++d) issue(d, d);
+    for (int t0 = 0; t0 < steps; t0 += DEPTH) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int dw = j >> 2, sh = 8 * (j & 3);
-                float f[8];
-#pragma unroll
-                for (int r = 0; r < 8; ++r) f[r] = (float)(int8_t)(wr[u][r][dw] >> sh);
-                u32x4_t b;
-                b[0] = pack_bf16x2(f[0], f[1]);
-                b[1] = pack_bf16x2(f[2], f[3]);
-                b[2] = pack_bf16x2(f[4], f[5]);
-                b[3] = pack_bf16x2(f[6], f[7]);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[u], __builtin_bit_cast(bf16x8_t, b),
-                                                                 acc[j], 0, 0, 0);
-            }
+        for (int d = 0; d < DEPTH; ++d) {
+            if (t0 + d < steps) convert_mfma(d);
+            // the step DEPTH ahead into the slot just used; past the last
+            // step these loads are out of range (no memory traffic)
+            issue(t0 + d + DEPTH, d);
         }
     }
 
@@ -176,17 +197,24 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     // Every wave writes its 16 accumulators ([wave][j][lane]: 1 KiB
     // contiguous per instruction); then wave w sums accumulators j = 2w and
     // 2w+1 over the 8 waves in wave order and owns that part of the
-    // workgroup's partial tile from here on.
+    // workgroup's partial tile from here on.  Only lanes holding rows < M
+    // (lane < 16 * ceil(M / 4)) take part: the rest hold the zero padding.
+    const int lanes_live = 16 * ((M + 3) / 4);
+    const bool live = lane < lanes_live;
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) red[(wave * 16 + j) * 64 + lane] = acc[j];
+        for (int j = 0; j < 16; ++j) red[(wave * 16 + j) * 64 + lane] = acc[j];
+    }
     lds_barrier();
-    f32x4_t r[2];
+    f32x4_t r[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    if (live) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int j = 2 * wave + h;
-        r[h] = red[j * 64 + lane];
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * wave + h;
+            r[h] = red[j * 64 + lane];
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) r[h] += red[(w * 16 + j) * 64 + lane];
+            for (int w = 1; w < WAVES; ++w) r[h] += red[(w * 16 + j) * 64 + lane];
+        }
     }
 
     // ---- partial tile out, then the last workgroup of the column tile ----
@@ -220,8 +248,6 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     // counter to 0 for the next call and reduces.  Exactly one workgroup
     // reduces.
     const int tiles = gridDim.x;
-    const int lanes_live = 16 * ((M + 3) / 4);  // lanes holding rows < M
-    const bool live = lane < lanes_live;
     {
         const __amdgpu_buffer_rsrc_t pr = part_rsrc(partials, split, tiles, tile, true);
         if (live) {
@@ -252,16 +278,16 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
         if (lane == 0) last = all;
     }
     lds_barrier();
-    if (!last || !live) return;
+    if (!last) return;
 
     // ---- reducer: y = act(scale * sum_p partials[p] + bias) for the tile ----
     // Wave w finishes accumulators j = 2w, 2w+1: lane (lc, lg) holds rows
     // 4*lg.. of column n0 + 16*lc + j.  The other splits' partials are
     // loaded (contiguous across lanes), its own is r[]; the sum is taken in
     // split order.  The loads are branch-free: a split that is absent or
-    // this workgroup's own gets an empty buffer range (the load returns 0
-    // without touching memory) and is replaced by a select, so the code
-    // stays short.
+    // this workgroup's own gets an empty buffer range, and a lane past the
+    // rows < M an out-of-range offset (the load returns 0 without touching
+    // memory); the absent and own splits are replaced by a select.
     f32x4_t pv[2][MAX_KS];
 #pragma unroll
     for (int p = 0; p < MAX_KS; ++p) {
@@ -269,7 +295,8 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             pv[h][p] = __builtin_bit_cast(
-                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(pr, ((2 * wave + h) * 64 + lane) * 16, 0, kSc1));
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             pr, live ? ((2 * wave + h) * 64 + lane) * 16 : kOOB, 0, kSc1));
     }
     // keep every load here, in flight together (the compiler would otherwise
     // sink some into the conditional sums below and wait for each in turn)
@@ -277,25 +304,34 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     for (int p = 0; p < MAX_KS; ++p)
 #pragma unroll
         for (int h = 0; h < 2; ++h) asm volatile("" : "+v"(pv[h][p]));
+    // The tile's outputs go through LDS ([m][256 columns] bf16, 8 KiB at
+    // most, in the reduction buffer: every wave has finished reading it) so
+    // that y is written with 8-byte stores of 4 consecutive columns.
+    uint16_t* stage = reinterpret_cast<uint16_t*>(red);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int c = n0 + 16 * lc + 2 * wave + h;
         f32x4_t sum = split == 0 ? r[h] : pv[h][0];
 #pragma unroll
         for (int p = 1; p < MAX_KS; ++p) {
             const f32x4_t v = p == split ? r[h] : pv[h][p];
             if (p < KS) sum += v;
         }
-        if (c >= N) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 4 * lg + i;
             if (m < M) {
                 float t = sum[i] * sc[h];
                 if (bias) t = t + bi[h];
-                y[(int64_t)m * N + c] = __builtin_bit_cast(uint16_t, (__bf16)activate<ACT>(t));
+                stage[m * COLS + 16 * lc + 2 * wave + h] = __builtin_bit_cast(uint16_t, (__bf16)activate<ACT>(t));
             }
         }
+    }
+    lds_barrier();
+    for (int e = tid; e < M * (COLS / 4); e += THREADS) {
+        const int m = e / (COLS / 4), q = e % (COLS / 4);
+        if (n0 + 4 * q < N)  // N % 16 == 0: a group of 4 columns is all in or all out
+            *reinterpret_cast<uint2*>(y + (int64_t)m * N + n0 + 4 * q) =
+                *reinterpret_cast<const uint2*>(stage + m * COLS + 4 * q);
     }
 }
 
