@@ -228,7 +228,8 @@ ExecutionArena::~ExecutionArena() {
 }
 void* ExecutionArena::allocateBytes(size_t bytes) {
     const size_t aligned_offset = (offset_ + 255) & ~size_t(255);
-    if (!buffer_ || aligned_offset + bytes > maxSize_) {
+    // written so that a huge request cannot wrap around the size check
+    if (!buffer_ || aligned_offset > maxSize_ || bytes > maxSize_ - aligned_offset) {
         record(JH_ERR_WORKSPACE);
         return nullptr;
     }

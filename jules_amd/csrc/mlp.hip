@@ -270,13 +270,14 @@ struct KPlan {
 };
 
 KPlan kplan(int M, int N, int K) {
-    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    // 64-bit: M, N, K may be anywhere up to INT_MAX
+    const int64_t tiles = ((int64_t)M + BM - 1) / BM * (((int64_t)N + BN - 1) / BN);
     const int max_s = K / (4 * BK);
-    if (tiles == 0 || tiles >= 128 || max_s < 2) return {1, K};
-    int S = (256 + tiles - 1) / tiles;
+    if (tiles <= 0 || tiles >= 128 || max_s < 2) return {1, K};
+    int S = (int)((256 + tiles - 1) / tiles);
     if (S > max_s) S = max_s;
-    const int kc = ((K + S - 1) / S + BK - 1) / BK * BK;
-    return {(K + kc - 1) / kc, kc};
+    const int64_t kc = (((int64_t)K + S - 1) / S + BK - 1) / BK * BK;
+    return {(int)(((int64_t)K + kc - 1) / kc), (int)kc};
 }
 
 size_t kplan_floats(int M, int N, int K) {

@@ -68,10 +68,10 @@ inline GemmTile f32_variant_tile(int v, int K) {
 // there are at least 512 of them (two per CU), else 32x32.
 inline GemmTile f32_gemm_tile(int M, int N, int K) {
     if ((int64_t)M * N <= (int64_t(1) << 20) && K <= kF32RowsMaxK) {
-        const bool one = (int64_t)((N + 63) / 64) * ((M + 1) / 2) < 1024;
+        const bool one = (((int64_t)N + 63) / 64) * (((int64_t)M + 1) / 2) < 1024;
         return f32_variant_tile(one ? GV_F32_ROWS1 : GV_F32_ROWS2, K);
     }
-    const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
+    const int64_t tiles64 = (((int64_t)M + 63) / 64) * (((int64_t)N + 63) / 64);
     return f32_variant_tile(tiles64 >= 512 ? GV_F32_T64 : GV_F32_T32, K);
 }
 

@@ -308,6 +308,8 @@ int main(int argc, char** argv) {
     char* p1 = static_cast<char*>(small.allocateBytes(100));
     CHECK(p1 == small.rawBuffer() + 4096 && small.usedBytes() == 4196);  // 256-byte aligned
     CHECK(small.allocateBytes(2 << 20) == nullptr && lastStatus() == JH_ERR_WORKSPACE);
+    // a request whose size would wrap the offset arithmetic is refused too
+    CHECK(small.allocateBytes(SIZE_MAX - 100) == nullptr && lastStatus() == JH_ERR_WORKSPACE);
     CHECK(small.usedBytes() == 4196 && small.highWaterMark() == 4196);
     hipPointerAttribute_t attr;
     CHECK(hipPointerGetAttributes(&attr, p0) == hipSuccess && attr.type == hipMemoryTypeDevice);
