@@ -39,9 +39,9 @@ PEAK = {"bf16": 2516.6, "f32": 157.3, "hbm": 8000.0, "int8": 5033.2}
 # counters read for a 64 MiB device copy (fetch x2.0, write x1.0).  They are
 # re-measured whenever a kernel changes; None where not measured.
 MEASURED_TRAFFIC = {
-    "c3": 201.7e6 + 33.9e6,   # gemm_bf16_dma_kernel<GELU>
-    "c4": 806.1e6 + 268.4e6,  # flash_fwd_bf16<128, causal>
-    "c5": 70.4e6 + 2.2e6,     # w8a16_splitk_kernel<SILU>
+    "c3": 201.7e6 + 33.8e6,   # gemm_bf16_dma_kernel<GELU>
+    "c4": 806.2e6 + 268.4e6,  # flash_fwd_bf16<128, causal>
+    "c5": 70.5e6 + 2.2e6,     # w8a16_splitk_kernel<SILU, flags>
 }
 
 
@@ -655,6 +655,10 @@ def main():
                     help="counter-collection workload for rocprofv3 --pmc: one 64 MiB device "
                          "copy of known size (calibration), 3 MFMA calibration launches, then 3 "
                          "launches of C3, C4 and C5")
+    ap.add_argument("--vendor", action="store_true",
+                    help="time the vendor library on C3's GEMM for comparison: torch.mm in bf16 "
+                         "at 4096^3 (hipBLASLt; GEMM only, no bias or GELU) beside this build's C3 "
+                         "kernel, and print one JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -664,6 +668,35 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     log = lambda m: print(f"[bench] {m}", file=sys.stderr, flush=True)  # noqa: E731
+
+    if args.vendor:
+        c = CONFIGS["c3"]
+        M, N, K = c["M"], c["N"], c["K"]
+        g = torch.Generator(device=dev).manual_seed(0)
+        A = torch.randn((M, K), generator=g, device=dev).mul_(K ** -0.5).to(torch.bfloat16)
+        B = torch.randn((K, N), generator=g, device=dev).mul_(K ** -0.5).to(torch.bfloat16)
+        out = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+        ours = Runner("c3", c, dev)
+        res = {}
+        for name, fn in (("torch.mm bf16 (hipBLASLt)", lambda: torch.mm(A, B, out=out)),
+                         ("jules_hip_gemm_bias_act bf16 + bias + GELU", ours.launch)):
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(20):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1) / 20)
+            ms = statistics.median(ts)
+            res[name] = {"ms": ms, "TFLOP/s": gemm_flops(M, N, K) / (ms * 1e-3) / 1e12}
+        print(json.dumps({"vendor_comparison": res, "shape": [M, N, K],
+                          "timing": "back-to-back launches on torch's current stream, median of 5 x 20"}))
+        return
 
     if args.pmc:
         src = torch.ones(64 << 20, dtype=torch.uint8, device=dev)
