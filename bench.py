@@ -8,7 +8,7 @@ synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 (2*M*N*K + 4*B*H*D*S*(S+1)/2 FLOP per step) over the timed steps.
 
 The same run also times every BASELINE config on its own (per_config, keys
-c1-c5), the reference's published fp32 GEMM shape (per_config, key g1,
+c1-c5; c5p is C5 on the packed weight layout), the reference's published fp32 GEMM shape (per_config, key g1,
 beside its published time), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
 entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
 (per_config, keys m1-m2, fp32 TFLOP/s), the flash-attention backward at C4's
@@ -42,6 +42,7 @@ MEASURED_TRAFFIC = {
     "c3": 201.7e6 + 33.8e6,   # gemm_bf16_dma_kernel<GELU>
     "c4": 806.2e6 + 268.4e6,  # flash_fwd_bf16<128, causal>
     "c5": 70.5e6 + 2.2e6,     # w8a16_splitk_kernel<SILU, flags>
+    "c5p": None,              # w8a16_packed_kernel<SILU, M <= 8>
 }
 
 
@@ -63,6 +64,12 @@ CONFIGS = {
     "c3": dict(kind="gemm", dtype="bf16", M=4096, N=4096, K=4096, act="gelu"),
     "c4": dict(kind="flash", dtype="bf16", B=8, H=32, S=4096, D=128, causal=True),
     "c5": dict(kind="w8a16", M=8, N=8192, K=8192, act="silu"),
+}
+
+# C5 on the packed weight layout (jules_hip_w8a16_packed_gemm_bias_act): the
+# same operation and data, W repacked once before timing (weight-load time).
+PACKED_CONFIGS = {
+    "c5p": dict(kind="w8a16", packed=True, M=8, N=8192, K=8192, act="silu"),
 }
 
 # Row kernels (the next rows of the hot-path scope; not BASELINE configs):
@@ -230,6 +237,9 @@ class Runner:
             self.bias = torch.rand((N,), generator=g, device=dev) * 0.2 - 0.1
             self.y = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
             self.ws = ops.w8a16_workspace(M, N, K, dev)
+            if s.get("packed"):
+                # repacked once, as at weight-load time; only the packed copies stay
+                self.W = [ops.w8a16_pack(W) for W in self.W]
             self.work = w8a16_bytes(M, N, K)
             self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK["hbm"]
         self.i = 0
@@ -255,6 +265,10 @@ class Runner:
                                                 out=getattr(self, "out", None))
         elif s["kind"] == "int8":
             ops.matmul_int8(self.A, self.W[self.i % self.nw], 0.013, 0.021, self.bias, out=self.C)
+            self.i += 1
+        elif s.get("packed"):
+            ops.w8a16_gemm_packed(self.x, self.W[self.i % self.nw], self.scale, self.bias, s["act"],
+                                  out=self.y)
             self.i += 1
         else:
             ops.w8a16_gemm(self.x, self.W[self.i % self.nw], self.scale, self.bias, s["act"],
@@ -312,6 +326,10 @@ class Runner:
         if k == "int8":
             return [(L.jules_hip_matmul_int8, (P(self.A), P(W), P(self.C), s["M"], s["N"], s["K"],
                                                0.013, 0.021, P(self.bias), st)) for W in self.W]
+        if s.get("packed"):
+            return [(L.jules_hip_w8a16_packed_gemm_bias_act,
+                     (act(s["act"]), P(self.x), P(W.data), P(self.scale), P(self.bias), P(self.y),
+                      s["M"], s["N"], s["K"], st)) for W in self.W]
         return [(L.jules_hip_w8a16_gemm_bias_act, (act(s["act"]), P(self.x), P(W), P(self.scale),
                                                    P(self.bias), P(self.y), s["M"], s["N"], s["K"],
                                                    P(self.ws), self.ws.numel(), st)) for W in self.W]
@@ -708,8 +726,8 @@ def main():
             c.launch()  # MFMA calibration dispatches (clock and MFMA busy under load)
         torch.cuda.synchronize()
         del c
-        for name in ("c3", "c4", "c5"):
-            r = Runner(name, CONFIGS[name], dev)
+        for name in ("c3", "c4", "c5", "c5p"):
+            r = Runner(name, {**CONFIGS, **PACKED_CONFIGS}[name], dev)
             for _ in range(3):
                 r.launch()
             torch.cuda.synchronize()
@@ -720,7 +738,8 @@ def main():
 
     # ---- per-config launch timings -----------------------------------------
     per = {}
-    ALL = {**CONFIGS, **GEMM_CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS, **INT8_CONFIGS}
+    ALL = {**CONFIGS, **PACKED_CONFIGS, **GEMM_CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS,
+           **INT8_CONFIGS}
     names = [n for n in ALL if not args.only or n in args.only.split(",")]
     if args.step_only:
         names = []
@@ -740,7 +759,7 @@ def main():
                          "single_p90_ms": d[(9 * len(d)) // 10],
                          "achieved": r.rate(med), "unit": r.unit, "peak": r.peak,
                          "frac": r.rate(med) / r.peak, "work": r.work, "spec": ALL[name]}
-            if name in ("c5", "i2"):
+            if name in ("c5", "c5p", "i2"):
                 # HBM-bound decode shapes: the plain streaming-read floor of
                 # the same weight bytes beside the kernel
                 if floor_ms is None:

@@ -216,6 +216,32 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W,
                                   void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* ---- W8A16 on packed weights ------------------------------------------------
+ * The same y = act(scale * x W + bias) as jules_hip_w8a16_gemm_bias_act, same
+ * constraints on M, N, K, x, scale, bias and y, with W first repacked once
+ * (at weight-load time) into a layout in which each workgroup streams one
+ * contiguous block: 32 output columns over all of K, in 1 KiB blocks per 32
+ * rows ordered as the kernel's MFMA operands (layout in w8a16_packed.hip).
+ * No split-K across workgroups, so no workspace and no cross-workgroup
+ * reduction; each tile's 8 wave partials are summed in a fixed order
+ * (deterministic; the order differs from the row-major entry point's, so
+ * the two agree to fp32 rounding, not bit for bit).
+ * jules_hip_w8a16_packed_size(K, N): bytes of the packed array
+ *   (ceil(N/32) * ceil(K/32) * 1024; 0 for K or N <= 0).
+ * jules_hip_w8a16_pack: W int8 [K,N] row-major (device) -> Wp (device,
+ *   16-byte aligned, packed_size bytes; rows past K and columns past N are
+ *   written as zero).  Same K, N limits as the GEMM.
+ * jules_hip_w8a16_packed_gemm_bias_act: Wp as written by jules_hip_w8a16_pack
+ *   with the same K and N.
+ * No reference counterpart (the reference has no W8A16 kernel); it is the
+ * decode configuration's fast path for callers that own their weights.
+ */
+size_t jules_hip_w8a16_packed_size(int K, int N);
+int jules_hip_w8a16_pack(const int8_t* W, int K, int N, void* Wp, size_t Wp_bytes, void* stream);
+int jules_hip_w8a16_packed_gemm_bias_act(int act, const void* x, const void* Wp,
+                                         const float* scale, const float* bias,
+                                         void* y, int M, int N, int K, void* stream);
+
 /* ---- W8A16 without allocation ------------------------------------------------
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -49,6 +49,10 @@ SIGNATURES = {
     "jules_hip_w8a16_workspace_size": (_size, [_int, _int, _int]),
     "jules_hip_w8a16_gemm_bias_act": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _int, _int, _int,
                                              _vp, _size, _vp]),
+    "jules_hip_w8a16_packed_size": (_size, [_int, _int]),
+    "jules_hip_w8a16_pack": (_int, [_vp, _int, _int, _vp, _size, _vp]),
+    "jules_hip_w8a16_packed_gemm_bias_act": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _int, _int,
+                                                    _int, _vp]),
     "jules_hip_w8a16_noalloc_max_bytes": (_size, []),
     "jules_hip_w8a16_gemm_bias_act_noalloc": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _int, _int,
                                                      _int, _vp]),

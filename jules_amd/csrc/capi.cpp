@@ -288,6 +288,43 @@ int jules_hip_w8a16_gemm_bias_act(int act, const void* x, const int8_t* W, const
                      "w8a16 launch");
 }
 
+size_t jules_hip_w8a16_packed_size(int K, int N) {
+    if (K <= 0 || N <= 0 || K > kMaxDecodeDim || N > kMaxDecodeDim || (int64_t)K * N > kMaxElems)
+        return 0;
+    return jh::w8a16_packed_bytes(K, N);
+}
+
+int jules_hip_w8a16_pack(const int8_t* W, int K, int N, void* Wp, size_t Wp_bytes, void* stream) {
+    if (K < 0 || N < 0) return fail(JH_ERR_SHAPE, "w8a16 pack: K=%d N=%d", K, N);
+    if (K == 0 || N == 0) return JH_OK;
+    if (N % 16 || K % 8 || N > kMaxDecodeDim || K > kMaxDecodeDim)
+        return fail(JH_ERR_UNSUPPORTED, "w8a16 pack: needs N%%16==0, K%%8==0, K,N<=2^26 (got %d %d)", K,
+                    N);
+    if ((int64_t)K * N > kMaxElems) return fail(JH_ERR_SHAPE, "w8a16 pack: too large");
+    if (!W || !Wp) return fail(JH_ERR_NULL, "w8a16 pack: null W or Wp");
+    if (!aligned(Wp, 16)) return fail(JH_ERR_ALIGN, "w8a16 pack: Wp 16-byte alignment");
+    const size_t need = jh::w8a16_packed_bytes(K, N);
+    if (Wp_bytes < need)
+        return fail(JH_ERR_WORKSPACE, "w8a16 pack: Wp holds %zu bytes, need %zu", Wp_bytes, need);
+    return check_hip(jh::launch_w8a16_pack(W, K, N, static_cast<int8_t*>(Wp),
+                                           static_cast<hipStream_t>(stream)),
+                     "w8a16 pack launch");
+}
+
+int jules_hip_w8a16_packed_gemm_bias_act(int act, const void* x, const void* Wp, const float* scale,
+                                         const float* bias, void* y, int M, int N, int K,
+                                         void* stream) {
+    bool done = false;
+    const int st = w8a16_check("w8a16 packed", act, x, static_cast<const int8_t*>(Wp), scale, bias, y,
+                               M, N, K, &done);
+    if (st != JH_OK || done) return st;
+    return check_hip(jh::launch_w8a16_packed(act, static_cast<const uint16_t*>(x),
+                                             static_cast<const int8_t*>(Wp), scale, bias,
+                                             static_cast<uint16_t*>(y), M, N, K,
+                                             static_cast<hipStream_t>(stream)),
+                     "w8a16 packed launch");
+}
+
 size_t jules_hip_w8a16_noalloc_max_bytes(void) { return jh::static_scratch_bytes(); }
 
 int jules_hip_w8a16_gemm_bias_act_noalloc(int act, const void* x, const int8_t* W,

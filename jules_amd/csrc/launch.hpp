@@ -53,6 +53,13 @@ size_t w8a16_partials_size(int M, int N, int K);
 hipError_t launch_w8a16_counters(int act, const uint16_t* x, const int8_t* W, const float* scale,
                                  const float* bias, uint16_t* y, int M, int N, int K,
                                  float* partials, uint32_t* counters, hipStream_t s);
+// W8A16 on the packed weight layout (w8a16_packed.hip): Wp holds
+// w8a16_packed_bytes(K, N) bytes, written by launch_w8a16_pack from
+// row-major W [K,N]
+size_t w8a16_packed_bytes(int K, int N);
+hipError_t launch_w8a16_pack(const int8_t* W, int K, int N, int8_t* Wp, hipStream_t s);
+hipError_t launch_w8a16_packed(int act, const uint16_t* x, const int8_t* Wp, const float* scale,
+                               const float* bias, uint16_t* y, int M, int N, int K, hipStream_t s);
 hipError_t launch_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                               float scale_a, float scale_b, const float* bias, hipStream_t s);
 hipError_t launch_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,

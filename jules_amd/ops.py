@@ -206,6 +206,54 @@ def w8a16_gemm(x, W, scale, bias=None, act="silu", out=None, workspace=None):
     return out
 
 
+class PackedW8:
+    """int8 weights [K,N] repacked for jules_hip_w8a16_packed_gemm_bias_act:
+    `data` is the packed uint8 array, K and N the logical shape."""
+
+    def __init__(self, data, K, N):
+        self.data, self.K, self.N = data, K, N
+
+
+def w8a16_pack(W):
+    """Repack int8 W [K,N] (row-major) into the packed W8A16 layout (done
+    once, at weight-load time)."""
+    _rank(W, "W", 2)
+    _need(W, "W", (torch.int8,))
+    _on_device(W=W)
+    K, N = W.shape
+    n = lib().jules_hip_w8a16_packed_size(K, N)
+    if n == 0:
+        raise ValueError(f"w8a16_pack: unsupported shape {tuple(W.shape)}")
+    Wp = torch.empty((n,), dtype=torch.uint8, device=W.device)
+    check(lib().jules_hip_w8a16_pack(_ptr(W), K, N, _ptr(Wp), n, _stream(W)))
+    return PackedW8(Wp, K, N)
+
+
+def w8a16_gemm_packed(x, Wp, scale, bias=None, act="silu", out=None):
+    """y = act(scale * (x @ W) + bias) with W given packed (w8a16_pack);
+    x bf16 [M,K]."""
+    if not isinstance(Wp, PackedW8):
+        raise TypeError("Wp must come from w8a16_pack")
+    _rank(x, "x", 2)
+    _need(x, "x", (torch.bfloat16,))
+    M, K = x.shape
+    N = Wp.N
+    if K != Wp.K:
+        raise ValueError("inner dimensions differ")
+    _need(Wp.data, "Wp", (torch.uint8,), numel=lib().jules_hip_w8a16_packed_size(K, N))
+    _need(scale, "scale", (torch.float32,), numel=N)
+    if bias is not None:
+        _need(bias, "bias", (torch.float32,), numel=N)
+    if out is not None:
+        _need(out, "out", (torch.bfloat16,), shape=(M, N))
+    _on_device(x=x, Wp=Wp.data, scale=scale, bias=bias, out=out)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    check(lib().jules_hip_w8a16_packed_gemm_bias_act(_act(act), _ptr(x), _ptr(Wp.data), _ptr(scale),
+                                                     _ptr(bias), _ptr(out), M, N, K, _stream(x)))
+    return out
+
+
 def _int8_operands(A, B, bias, out):
     _rank(A, "A", 2)
     _rank(B, "B", 2)

@@ -363,3 +363,30 @@ def test_hbm_read_floor_validation():
     assert f(P, (1 << 20) + 8, P, 256, None) == SHAPE
     assert f(P, 0, P, 256, None) == SHAPE
     assert f(P, 1 << 20, P, 0, None) == SHAPE
+
+
+def test_w8a16_packed_validation():
+    """Packed W8A16: the packed size, the pack's argument checks and the GEMM's
+    (the same as the row-major entry point's), all before any device work."""
+    L = _lib.lib()
+    assert L.jules_hip_w8a16_packed_size(8192, 8192) == 8192 * 8192
+    assert L.jules_hip_w8a16_packed_size(40, 272) == 9 * 2 * 1024
+    assert L.jules_hip_w8a16_packed_size(0, 64) == 0
+    assert L.jules_hip_w8a16_packed_size(64, -16) == 0
+    pack = L.jules_hip_w8a16_pack
+    assert pack(P, -1, 64, P, 1 << 20, None) == SHAPE
+    assert pack(None, 0, 64, None, 0, None) == OK
+    assert pack(P, 64, 40, P, 1 << 20, None) == UNSUP
+    assert pack(P, 60, 64, P, 1 << 20, None) == UNSUP
+    assert pack(None, 64, 64, P, 1 << 20, None) == NULL
+    assert pack(P, 64, 64, None, 1 << 20, None) == NULL
+    assert pack(P, 64, 64, P + 8, 1 << 20, None) == ALIGN
+    assert pack(P, 64, 64, P, 64 * 64 - 1, None) == WS
+    f = L.jules_hip_w8a16_packed_gemm_bias_act
+    assert f(9, P, P, P, None, P, 8, 64, 64, None) == ACT
+    assert f(5, P, P, P, None, P, 17, 64, 64, None) == UNSUP
+    assert f(5, P, P, P, None, P, 8, 40, 64, None) == UNSUP
+    assert f(5, P, P, P, None, P, 8, 64, 60, None) == UNSUP
+    assert f(5, None, P, P, None, P, 8, 64, 64, None) == NULL
+    assert f(5, P, P + 4, P, None, P, 8, 64, 64, None) == ALIGN
+    assert f(5, None, None, None, None, None, 0, 64, 64, None) == OK
