@@ -47,18 +47,24 @@ constexpr float kNegInf = -__builtin_huge_valf();
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
 // Workgroup -> (head, query tile).  Workgroups are dealt to the 8 XCDs round
-// robin; the mapping gives each XCD whole heads (head = 8*j + xcd), all query
-// tiles of a head in a row, heaviest (causal) first.  The ~64 workgroups an
-// XCD runs at once then span about two heads, whose K and V (2 MiB each at
-// S=4096, D=128) stay in that XCD's 4 MiB L2 instead of being re-read from
-// HBM by every query tile.
+// robin; the mapping gives each XCD whole heads (head = 8*j + xcd), taken in
+// pairs: the query tiles of heads j = 2g and 2g+1 are interleaved, heaviest
+// (causal: most keys) first.  The workgroups an XCD runs at once then span
+// about two heads, whose K and V (2 MiB each at S=4096, D=128) stay in that
+// XCD's 4 MiB L2 instead of being re-read from HBM by every query tile, and
+// consecutive workgroups shrink in size across the pair, so the CUs that
+// finish early take the next heavy ones (one head at a time, heaviest first,
+// left a ~5 % tail of CUs idle behind the last heads' heavy tiles).
 __device__ __forceinline__ void block_coords(int BH, int nq, int bq, int* bh, int* q0) {
     const int b = blockIdx.x;
     int head, qi;
     if ((BH & 7) == 0) {
         const int xcd = b & 7, i = b >> 3;
-        head = 8 * (i / nq) + xcd;
-        qi = i % nq;
+        const int J = BH >> 3;                   // heads of this XCD
+        const int g = i / (2 * nq), r = i - g * 2 * nq;
+        const int gs = min(2, J - 2 * g);        // heads in this pair (1 for an odd last one)
+        head = 8 * (2 * g + r % gs) + xcd;
+        qi = r / gs;
     } else {
         head = b / nq;
         qi = b % nq;
