@@ -52,6 +52,26 @@ constexpr int BT = BW * 64;      // threads per workgroup
 constexpr int BOWN = BW * 32;    // keys (dK/dV pass) or queries (dQ pass) a workgroup owns
 constexpr int BSTEP = 64;        // query (dK/dV) or key (dQ) rows per loop step
 
+// Workgroup -> (head, block rank), rank 0 the block with the longest causal
+// range.  The forward's order: workgroups are dealt to the 8 XCDs round robin,
+// each XCD takes whole heads (head = 8*j + xcd) two at a time with their
+// blocks interleaved, longest first, so the heads' operands stay in that XCD's
+// L2 and the CUs that finish early take the next long blocks.
+__device__ __forceinline__ void bwd_block(int nblk, int* bh, int* rank) {
+    const int b = blockIdx.x, BH = gridDim.x / nblk;
+    if ((BH & 7) == 0) {
+        const int xcd = b & 7, i = b >> 3;
+        const int J = BH >> 3;
+        const int g = i / (2 * nblk), r = i - g * 2 * nblk;
+        const int gs = min(2, J - 2 * g);
+        *bh = 8 * (2 * g + r % gs) + xcd;
+        *rank = r / gs;
+    } else {
+        *bh = b / nblk;
+        *rank = b % nblk;
+    }
+}
+
 template <int D>
 struct BwdCfg {
     static constexpr int PITCH = D * 2 + 16;   // bytes per LDS row
@@ -264,8 +284,9 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
     const int nkb = (S + BOWN - 1) / BOWN;
-    const int bh = blockIdx.x / nkb;
-    const int k0 = (blockIdx.x % nkb) * BOWN;  // longest causal range (first keys) first
+    int bh, rank;
+    bwd_block(nkb, &bh, &rank);
+    const int k0 = rank * BOWN;  // longest causal range (first keys) first
     const int64_t hoff = (int64_t)bh * S * D;
     const uint16_t* Qh = Q + hoff;
     const uint16_t* Oh = dO + hoff;
@@ -419,8 +440,9 @@ __global__ __launch_bounds__(QT, 1) void flash_bwd_dq_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, col = lane & 31;
     const int nqb = (S + QOWN - 1) / QOWN;
-    const int bh = blockIdx.x / nqb;
-    const int q0 = (nqb - 1 - blockIdx.x % nqb) * QOWN;  // longest causal range first
+    int bh, rank;
+    bwd_block(nqb, &bh, &rank);
+    const int q0 = (nqb - 1 - rank) * QOWN;  // longest causal range first
     const int64_t hoff = (int64_t)bh * S * D;
     const uint16_t* Kh = K + hoff;
     const uint16_t* Vh = V + hoff;
