@@ -254,7 +254,7 @@ __device__ __forceinline__ void flash_bf16_body(
     using C = Bf16Cfg<D>;
     constexpr int BKV = C::BKV;
     constexpr float kLazy = 8.0f;
-    constexpr int LA = 8;                       // MFMAs whose LDS reads are in flight (at most 15 reads)
+    constexpr int LA = 5;                       // MFMAs whose LDS reads are in flight (at most 15 reads)
     constexpr int KR = LA + 2, VR = LA + 2;     // K / V fragment ring sizes
     constexpr int PIECES = 2 * C::SEGW;         // copy instructions per wave per tile
     __shared__ __attribute__((aligned(1024))) uint8_t sm[C::NSTAGE * C::STAGE];
