@@ -20,12 +20,14 @@
 // i.e. exactly the B operands of the two v_mfma_f32_16x16x32_bf16 of that
 // k-step (column j and column 16 + j, k = 8 kg .. 8 kg + 7).  Rows past K and
 // columns past N are zero.  ksteps = ceil(K / 32), tiles = ceil(N / 32).
-// Blocks are k-step-major, and wave w of every workgroup takes k-steps w,
-// w + 4, w + 8, ...: at any moment the whole grid reads one contiguous window
-// of W, the access pattern of a plain streaming read.
+// Blocks are k-step-major, and wave w of every workgroup takes k-steps in
+// adjacent pairs, 2w, 2w + 1, 2w + 8, 2w + 9, ...: at any moment the whole
+// grid reads one contiguous window of W, the access pattern of a plain
+// streaming read, and one x load of a pair covers whole 128-byte lines of x.
 //
-// Per workgroup (4 waves), each wave keeps 8 k-steps of weight loads in
-// flight (32 KiB per CU; more in flight was measured slower).  Each step
+// Per workgroup (4 waves), each wave issues the weight loads of the k-steps 6
+// ahead before it converts the current pair, so 6 to 8 steps (24-32 KiB per
+// CU) are in flight; more in flight was measured slower.  Each step
 // converts the lane's 16 weight bytes to bf16 in registers (int8 is exact in
 // bf16) and issues two MFMAs with x (M padded to 16 rows) as the A operand.
 // For M <= 8 one x load serves two k-steps (see XP below).  The 4 wave
@@ -41,8 +43,9 @@ constexpr int PK_COLS = 32;     // columns per tile (one workgroup)
 constexpr int PK_KSTEP = 32;    // rows per k-step
 constexpr int PK_WAVES = 4;
 constexpr int PK_THREADS = PK_WAVES * 64;
-constexpr int PK_DEPTH = 8;     // k-steps of weight loads in flight per wave
-constexpr int kNTp = 2;         // buffer cache policy: nontemporal (streamed once)
+constexpr int PK_DEPTH = 6;     // k-steps of weight loads issued ahead per wave
+// W loads use the default cache policy: the nontemporal hint measured ~1 %
+// slower on this read stream
 constexpr uint32_t kOOBp = 0x80000000u;  // past every buffer range used: loads return 0
 // byte offset of block (tile c, k-step s)
 __host__ __device__ __forceinline__ int64_t pk_block(int c, int s, int tiles) {
@@ -102,10 +105,12 @@ __global__ __launch_bounds__(PK_THREADS, 1) void w8a16_packed_kernel(
     const float esc = scale[min(ecol, N - 1)];
     const float ebi = bias ? bias[min(ecol, N - 1)] : 0.0f;
 
-    // this wave's k-steps: s(t) = wave + PK_WAVES * t for t < n
+    // this wave's k-steps, in adjacent pairs: s(t) = 8 (t / 2) + 2 wave + t % 2
+    // for t < n (every s < ksteps exactly once over the 4 waves)
     const int tiles = gridDim.x;
-    const int s0 = wave;
-    const int n = ksteps > wave ? (ksteps - wave + PK_WAVES - 1) / PK_WAVES : 0;
+    const int full = ksteps >> 3, rest = ksteps & 7;
+    const int n = 2 * full + min(max(rest - 2 * wave, 0), 2);
+    auto kstep = [&](int t) { return 2 * PK_WAVES * (t >> 1) + 2 * wave + (t & 1); };
     const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(x), 0, (uint32_t)M * (uint32_t)K * 2u, 0x00020000);
 
@@ -114,21 +119,25 @@ __global__ __launch_bounds__(PK_THREADS, 1) void w8a16_packed_kernel(
     // serves two k-steps: lanes j < 8 fetch row j of step t, lanes j >= 8 row
     // j - 8 of step t + 1; step t keeps the low lanes (the high ones zeroed),
     // step t + 1 gets the high lanes' data moved down by a DPP row shift.
-    constexpr int XSLOTS = XP ? PK_DEPTH / 2 : PK_DEPTH;
-    u32x4_t wr[PK_DEPTH], xr[XSLOTS];
+    // step t lives in slot t % RING: PK_DEPTH steps ahead plus the pair (or
+    // step) being converted
+    constexpr int STEP = XP ? 2 : 1;
+    constexpr int RING = PK_DEPTH + STEP;
+    constexpr int XSLOTS = XP ? RING / 2 : RING;
+    u32x4_t wr[RING], xr[XSLOTS];
     auto wload = [&](int t, int d) {
         const bool live = t < n;
         const __amdgpu_buffer_rsrc_t wsrc = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int8_t*>(Wp) + (live ? pk_block(tile, s0 + t * PK_WAVES, tiles) : 0), 0,
+            const_cast<int8_t*>(Wp) + (live ? pk_block(tile, kstep(t), tiles) : 0), 0,
             live ? 1024u : 0u, 0x00020000);
-        wr[d] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, lane * 16, 0, kNTp);
+        wr[d] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, lane * 16, 0, 0);
     };
     // x fragment of local step t, row r, into slot xd.  Range-checked buffer
     // loads stand in for every bounds test: steps past n are past the weight
     // range, x rows past M and k past K get an out-of-range offset; all
     // return 0.
     auto xload = [&](int t, int r, int xd) {
-        const int kb = PK_KSTEP * (s0 + t * PK_WAVES) + 8 * kg;
+        const int kb = PK_KSTEP * kstep(t) + 8 * kg;
         const uint32_t xo = (r < M && t < n && kb < K) ? (uint32_t)(r * K + kb) * 2u : kOOBp;
         xr[xd] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, xo, 0, 0);
     };
@@ -173,16 +182,15 @@ __global__ __launch_bounds__(PK_THREADS, 1) void w8a16_packed_kernel(
             if (t < n) mfma2(xr[d], d);
         }
     };
-    constexpr int STEP = XP ? 2 : 1;
-
 #pragma unroll
     for (int d = 0; d < PK_DEPTH; d += STEP) issue(d, d);
-    for (int t0 = 0; t0 < n; t0 += PK_DEPTH) {
+    for (int t0 = 0; t0 < n; t0 += RING) {
 #pragma unroll
-        for (int d = 0; d < PK_DEPTH; d += STEP) {
+        for (int d = 0; d < RING; d += STEP) {
+            // the steps PK_DEPTH ahead (past n: no traffic) into the slot the
+            // previous pair freed, then the current pair
+            issue(t0 + d + PK_DEPTH, (d + PK_DEPTH) % RING);
             convert(t0 + d, d);
-            // the steps PK_DEPTH ahead into the slots just used (past n: no traffic)
-            issue(t0 + d + PK_DEPTH, d);
         }
     }
 
