@@ -31,8 +31,8 @@
 // converts the lane's 16 weight bytes to bf16 in registers (int8 is exact in
 // bf16) and issues two MFMAs with x (M padded to 16 rows) as the A operand.
 // For M <= 8 one x load serves two k-steps (see XP below).  The 4 wave
-// partials are summed in LDS in wave order (deterministic), then scale, bias
-// and the activation are applied and y is stored.
+// partials are summed in LDS in wave order (deterministic); every thread then
+// finishes one output (two for M > 8): scale, bias, activation, bf16 store.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -99,9 +99,12 @@ __global__ __launch_bounds__(PK_THREADS, 1) void w8a16_packed_kernel(
     const int n0 = tile * PK_COLS;
     const int j = lane & 15, kg = lane >> 4;
 
-    // epilogue operands of the column this lane finishes (waves 0 and 1),
-    // loaded now so their latency is off the tail
-    const int ecol = n0 + 16 * (wave & 1) + j;
+    // The epilogue gives every thread one output of rows 0-7 (and one of rows
+    // 8-15 when M > 8): half eh = tid / 128 (columns 16 eh .. 16 eh + 15),
+    // row em = (tid / 16) % 8, column ej = tid % 16.  Its scale and bias are
+    // loaded now so their latency is off the tail.
+    const int eh = tid >> 7, em = (tid >> 4) & 7, ej = tid & 15;
+    const int ecol = n0 + 16 * eh + ej;
     const float esc = scale[min(ecol, N - 1)];
     const float ebi = bias ? bias[min(ecol, N - 1)] : 0.0f;
 
@@ -194,23 +197,29 @@ __global__ __launch_bounds__(PK_THREADS, 1) void w8a16_packed_kernel(
         }
     }
 
-    // ---- the 8 wave partials, summed in wave order; wave h finishes half h ----
+    // ---- the 4 wave partials of each output, summed in wave order ----
 #pragma unroll
     for (int h = 0; h < 2; ++h) red[(wave * 2 + h) * 64 + lane] = acc[h];
     pk_lds_barrier();
-    if (wave >= 2) return;
-    f32x4_t sum = red[wave * 64 + lane];
+    // Output (row m, column 16 eh + ej) sits in component m % 4 of lane
+    // 16 (m / 4) + ej of each wave's half-eh accumulator.  Rows past M hold 0;
+    // range-checked buffer stores drop them and columns past N without
+    // branches (M * N * 2 <= 2^31: every offset fits the 32-bit range).
+    const float* redf = reinterpret_cast<const float*>(red);
+    const __amdgpu_buffer_rsrc_t ysrc =
+        __builtin_amdgcn_make_buffer_rsrc(y, 0, (uint32_t)M * (uint32_t)N * 2u, 0x00020000);
 #pragma unroll
-    for (int w = 1; w < PK_WAVES; ++w) sum += red[(w * 2 + wave) * 64 + lane];
-    if (ecol >= N) return;
+    for (int r = 0; r < (XP ? 1 : 2); ++r) {
+        const int m = em + 8 * r;
+        const int src = ((m >> 2) * 16 + ej) * 4 + (m & 3);
+        float sum = redf[eh * 256 + src];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * kg + i;
-        if (m < M) {
-            float t = sum[i] * esc;
-            if (bias) t = t + ebi;
-            y[(int64_t)m * N + ecol] = __builtin_bit_cast(uint16_t, (__bf16)activate<ACT>(t));
-        }
+        for (int w = 1; w < PK_WAVES; ++w) sum += redf[(w * 2 + eh) * 256 + src];
+        float t = sum * esc;
+        if (bias) t = t + ebi;
+        const uint32_t yo = (m < M && ecol < N) ? (uint32_t)(m * N + ecol) * 2u : kOOBp;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)activate<ACT>(t)),
+                                              ysrc, yo, 0, 0);
     }
 }
 
