@@ -419,16 +419,19 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
 }
 
 // ---- 3. dQ ----------------------------------------------------------------------
-// 8 waves x 32 queries (two waves per SIMD).  K/V tiles of 64 keys are double
-// buffered in LDS: the global loads of tile t+1 are issued into registers
-// before tile t is multiplied and stored to the other buffer after, one
-// barrier per tile.
-constexpr int QW = 8;             // waves per dQ workgroup
+// 4 waves x 32 queries, two workgroups per CU: the two waves of a SIMD come
+// from different workgroups, whose barriers are independent, so one's MFMAs
+// overlap the other's exp and dS arithmetic (8-wave workgroups kept both in
+// step and measured 1-3 % slower).  K/V tiles of 64 keys are double buffered
+// in LDS: the global loads of tile t+1 are issued into registers before tile
+// t is multiplied and stored to the other buffer after, one barrier per tile.
+// Causal: a wave skips the tiles wholly above its last query.
+constexpr int QW = 4;             // waves per dQ workgroup
 constexpr int QT = QW * 64;
 constexpr int QOWN = QW * 32;     // queries per dQ workgroup
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(QT, 1) void flash_bwd_dq_kernel(
+__global__ __launch_bounds__(QT, 2) void flash_bwd_dq_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dvec,
     uint16_t* __restrict__ dQ, int S, float scale) {
@@ -438,6 +441,7 @@ __global__ __launch_bounds__(QT, 1) void flash_bwd_dq_kernel(
     __shared__ __attribute__((aligned(16))) uint8_t kv_t[2][2][BSTEP * C::PITCH];  // [buf][K, V]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const int g = lane >> 5, col = lane & 31;
     const int nqb = (S + QOWN - 1) / QOWN;
     int bh, rank;
@@ -495,6 +499,8 @@ __global__ __launch_bounds__(QT, 1) void flash_bwd_dq_kernel(
         if (t + 1 < nt) gload(kb + BSTEP);
         const uint8_t* k_t = kv_t[buf][0];
         const uint8_t* v_t = kv_t[buf][1];
+        // causal: a tile wholly above this wave's last query adds nothing
+        if (!CAUSAL || kb <= q0 + wave_u * 32 + 31) {
         // S^T = K Q^T, dP^T = V dO^T: 64 keys x this wave's 32 queries
         bf16x8_t sb[2][2];  // dS^T as B operands: [32-key half][16-key step]
 #pragma unroll
@@ -528,6 +534,7 @@ __global__ __launch_bounds__(QT, 1) void flash_bwd_dq_kernel(
                 constexpr int m = decltype(mi)::value, dt = m >> 2, h = (m >> 1) & 1, t2 = m & 1;
                 dq[dt] = mfma(a, sb[h][t2], dq[dt]);
             });
+        }
         if (t + 1 < nt) sstore(buf ^ 1);
         __syncthreads();
     }
