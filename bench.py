@@ -8,8 +8,9 @@ synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 (2*M*N*K + 4*B*H*D*S*(S+1)/2 FLOP per step) over the timed steps.
 
 The same run also times every BASELINE config on its own (per_config, keys
-c1-c5; c5p is C5 on the packed weight layout), the reference's published fp32 GEMM shape (per_config, key g1,
-beside its published time), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
+c1-c5; c5p is C5 on the packed weight layout), the reference's published shapes (per_config, keys
+g1-g3: fp32 matmuls, a1: fp32 non-causal flash attention; each beside its published time and the
+ratio to it), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
 entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
 (per_config, keys m1-m2, fp32 TFLOP/s), the flash-attention backward at C4's
 shape (per_config, key b4), matmulInt8 (per_config, keys i1-i2: int8 TOP/s at
@@ -91,6 +92,18 @@ ROW_CONFIGS = {
 GEMM_CONFIGS = {
     "g1": dict(kind="gemm", dtype="f32", M=64, N=256, K=784, act="none", bias=False,
                reference_published_ms=0.090),
+    # the other two published matmul shapes (bench_comparison.py:143-144)
+    "g2": dict(kind="gemm", dtype="f32", M=64, N=10, K=256, act="none", bias=False,
+               reference_published_ms=0.008),
+    "g3": dict(kind="gemm", dtype="f32", M=128, N=512, K=512, act="none", bias=False,
+               reference_published_ms=0.141),
+}
+
+# The reference's published flash-attention time (bench_comparison.py:215):
+# fp32, non-causal, [B=2, H=8, S=1024, D=64], 135.416 ms on four AVX-512 cores.
+FLASH_REF_CONFIGS = {
+    "a1": dict(kind="flash", dtype="f32", B=2, H=8, S=1024, D=64, causal=False,
+               reference_published_ms=135.416),
 }
 
 
@@ -738,8 +751,8 @@ def main():
 
     # ---- per-config launch timings -----------------------------------------
     per = {}
-    ALL = {**CONFIGS, **PACKED_CONFIGS, **GEMM_CONFIGS, **ROW_CONFIGS, **MLP_CONFIGS, **BWD_CONFIGS,
-           **INT8_CONFIGS}
+    ALL = {**CONFIGS, **PACKED_CONFIGS, **GEMM_CONFIGS, **FLASH_REF_CONFIGS, **ROW_CONFIGS,
+           **MLP_CONFIGS, **BWD_CONFIGS, **INT8_CONFIGS}
     names = [n for n in ALL if not args.only or n in args.only.split(",")]
     if args.step_only:
         names = []
@@ -759,6 +772,12 @@ def main():
                          "single_p90_ms": d[(9 * len(d)) // 10],
                          "achieved": r.rate(med), "unit": r.unit, "peak": r.peak,
                          "frac": r.rate(med) / r.peak, "work": r.work, "spec": ALL[name]}
+            if "reference_published_ms" in ALL[name]:
+                # the reference's own published time for this shape (other
+                # hardware: four AVX-512 cores), and the ratio to it
+                pub = ALL[name]["reference_published_ms"]
+                per[name]["reference_published_ms"] = pub
+                per[name]["speedup_vs_published"] = pub / med
             if name in ("c5", "c5p", "i2"):
                 # HBM-bound decode shapes: the plain streaming-read floor of
                 # the same weight bytes beside the kernel
