@@ -349,8 +349,17 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void cross_entr
     const int nv = N & ~15;
     const float pt = row_norm(row_exp(xt - mx, t, nv), 1.0f / s, s, t, nv);
     const float fm = (float)M;
+    // grad / M as the reference's division; for a power-of-two M the product
+    // with 1/M (exact) is the same single rounding of x * 2^-k, bit for bit,
+    // at a tenth of the instructions
+    if ((M & (M - 1)) == 0) {
+        const float rm = 1.0f / fm;
 #pragma unroll
-    for (int k = 0; k < ELEMS; ++k) R.v[k] = R.v[k] / fm;
+        for (int k = 0; k < ELEMS; ++k) R.v[k] = R.v[k] * rm;
+    } else {
+#pragma unroll
+        for (int k = 0; k < ELEMS; ++k) R.v[k] = R.v[k] / fm;
+    }
     R.store(g, N, tid);
     if (owner) {
         g[t] = (pt - 1.0f) / fm;  // after this thread's own store of g[t]
@@ -376,7 +385,12 @@ __global__ __launch_bounds__(LT) void cross_entropy_long_kernel(const float* log
     long_row_stats(x, N, red, &mx, &s);
     const float inv = 1.0f / s;
     const float fm = (float)M;
-    row_loop(N, [&](int j) { g[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv) / fm; });
+    if ((M & (M - 1)) == 0) {  // exact product with 1/M, as in cross_entropy_kernel
+        const float rm = 1.0f / fm;
+        row_loop(N, [&](int j) { g[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv) * rm; });
+    } else {
+        row_loop(N, [&](int j) { g[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv) / fm; });
+    }
     if (owner) {
         const float pt = row_norm(row_exp(xt - mx, t, nv), inv, s, t, nv);
         g[t] = (pt - 1.0f) / fm;  // after this thread's own store of g[t]
@@ -386,16 +400,39 @@ __global__ __launch_bounds__(LT) void cross_entropy_long_kernel(const float* log
     }
 }
 
-// loss = sum of row_loss in a fixed order / M (one workgroup)
-__global__ __launch_bounds__(256) void cross_entropy_reduce_kernel(const float* __restrict__ row_loss,
-                                                                   float* __restrict__ loss, int M) {
-    __shared__ float part[4];
+// loss = sum of row_loss in a fixed order / M (one workgroup of RT threads).
+// Thread i adds rows i, i + RT, i + 2 RT, ..., RU of them per round with all
+// RU loads in flight together (a loop of dependent load-add steps waited out
+// one memory latency per row: ~25 us at M = 16384); then a butterfly within
+// each wave and a fixed tree over the wave sums.
+constexpr int RT = 1024, RU = 16;
+__global__ __launch_bounds__(RT) void cross_entropy_reduce_kernel(const float* __restrict__ row_loss,
+                                                                  float* __restrict__ loss, int M) {
+    __shared__ float part[RT / 64];
     float s = 0.0f;
-    for (int i = threadIdx.x; i < M; i += 256) s += row_loss[i];
+    for (int i0 = threadIdx.x; i0 < M; i0 += RT * RU) {
+        float v[RU];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            const int i = i0 + RT * u;
+            v[u] = i < M ? row_loss[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < RU; ++u) s += v[u];
+    }
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
-    if (threadIdx.x == 0) loss[0] = ((part[0] + part[1]) + (part[2] + part[3])) / (float)M;
+    if (threadIdx.x == 0) {
+        float w[RT / 64];
+#pragma unroll
+        for (int i = 0; i < RT / 64; ++i) w[i] = part[i];
+#pragma unroll
+        for (int h = RT / 128; h > 0; h >>= 1)
+#pragma unroll
+            for (int i = 0; i < h; ++i) w[i] = w[i] + w[i + h];
+        loss[0] = w[0] / (float)M;
+    }
 }
 
 // Launch plan for a row length: the smallest register-held size that fits
@@ -501,7 +538,7 @@ hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, flo
         }
     }
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(cross_entropy_reduce_kernel, dim3(1), dim3(256), 0, s, row_loss, loss, M);
+    hipLaunchKernelGGL(cross_entropy_reduce_kernel, dim3(1), dim3(RT), 0, s, row_loss, loss, M);
     return hipGetLastError();
 }
 
