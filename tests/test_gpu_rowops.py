@@ -101,6 +101,27 @@ def test_cross_entropy(dev, M, N):
     assert abs(loss - lr) <= 2e-6 * max(1.0, abs(lr))
 
 
+@pytest.mark.parametrize("M,N", [(40000, 8), (16384, 16), (20001, 12)])
+def test_cross_entropy_many_rows(dev, M, N):
+    """More rows than the loss reduction's 1024 threads x 16 loads (a second
+    round), at a power-of-two M (gradient by the product with 1/M) and two
+    others (the division)."""
+    case(f"cross entropy many rows [{M},{N}]")
+    x = _x(M, N, M + N)
+    t = np.random.default_rng(M).integers(0, N, M).astype(np.int32)
+    loss, g = ops.cross_entropy(to_dev(x, torch.float32, dev), to_dev(t, torch.int32, dev))
+    loss, g = float(to_np(loss)[0]), to_np(g)
+    loss64, g64 = po.cross_entropy64(x, t)
+    assert abs(loss - loss64) <= I.TOL["f32"] * max(1.0, abs(loss64))
+    assert I.rel_err(g, g64) < I.TOL["f32"]
+    # the gradient is (p - onehot) / M with the reference's rounding: exactly
+    # the restatement's division of the kernel's own p - onehot
+    xt = to_dev(x, torch.float32, dev)
+    p = ops.softmax(xt).cpu().numpy()
+    p[np.arange(M), t] -= np.float32(1.0)
+    np.testing.assert_array_equal(g, (p / np.float32(M)).astype(np.float32))
+
+
 def test_cross_entropy_bad_target_and_repeat(dev):
     """An out-of-range target gives a NaN loss (the reference reads out of
     bounds); the workspace is reused across calls without stale data."""

@@ -66,9 +66,13 @@ def test_c5_full_size(dev):
     assert (d <= 2.0 ** -7 * np.abs(y) + 2e-5 * np.abs(y).max()).all()
 
 
+# k-steps of 32 are dealt to the 4 waves in adjacent pairs (8 per round):
+# the shapes cover every remainder of ksteps % 8 (K = 352: 11 steps, 480: 15,
+# 192: 6 steps, no full round) and M on both sides of the paired-x path
 @pytest.mark.parametrize("M,N,K", [(1, 16, 8), (3, 272, 40), (8, 512, 1000), (9, 256, 4096),
                                    (16, 1040, 2056), (8, 8192, 64), (5, 4096, 33000),
-                                   (2, 48, 264)])
+                                   (2, 48, 264), (3, 160, 352), (7, 96, 480), (1, 16, 192),
+                                   (12, 64, 480), (8, 32, 136), (4, 48, 384)])
 def test_shapes_against_fp64(dev, M, N, K):
     case(f"w8a16 packed {M}x{N}x{K}")
     x, W, scale, bias = I.w8a16_inputs(M, N, K, seed=M + N + K)
