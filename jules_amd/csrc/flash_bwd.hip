@@ -294,6 +294,7 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
 
     // this lane's key (S / dP column) and its K row (B operand of S)
     const int key = k0 + wave * 32 + col;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const int kr = min(key, S - 1);
     bf16x8_t kf[C::KS];
 #pragma unroll
@@ -347,6 +348,8 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
         const float* lse_t = ld_t[buf][0];
         const float* dv_t = ld_t[buf][1];
 
+        // every query of the step is < S and (causal) after every key of the wave
+        const bool unmasked = q0 + KVSTEP <= S && (!CAUSAL || k0 + wave_u * 32 + 31 <= q0);
         // S = Q K^T and dP = dO V^T for the 32 queries x this wave's 32 keys
         bf16x8_t pa[1][2], sa[1][2];  // P and dS as A operands: [16-query step]
 #pragma unroll
@@ -359,7 +362,12 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
                 s = mfma(row_frag<D>(q_t, h * 32 + col, ks, g), kf[ks], s);
                 dp = mfma(row_frag<D>(do_t, h * 32 + col, ks, g), row_frag<D>(v_t, vrow, ks, g), dp);
             }
-            // register r: query 8(r/4) + 4g + r%4 of this block
+            // register r: query 8(r/4) + 4g + r%4 of this block.  Every step
+            // computes P and dS unmasked; only the last block and the
+            // diagonal then zero the masked elements (queries past S, causal
+            // keys after the query).  The
+            // per-element compares and selects on every step were ~a quarter
+            // of the step's vector work.
             float p[16], ds[16];
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
@@ -368,11 +376,20 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
                 const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&dv_t[ql]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int r = 4 * r4 + i, q = q0 + ql + i;
-                    const bool live = q < S && (!CAUSAL || key <= q);
-                    const float pv = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -l4[i])) : 0.0f;
+                    const int r = 4 * r4 + i;
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -l4[i]));
                     p[r] = pv;
                     ds[r] = pv * (dp[r] - d4[i]);
+                }
+            }
+            if (!unmasked) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int q = q0 + h * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (!(q < S && (!CAUSAL || key <= q))) {
+                        p[r] = 0.0f;
+                        ds[r] = 0.0f;
+                    }
                 }
             }
 #pragma unroll
@@ -501,6 +518,9 @@ __global__ __launch_bounds__(QT, 2) void flash_bwd_dq_kernel(
         const uint8_t* v_t = kv_t[buf][1];
         // causal: a tile wholly above this wave's last query adds nothing
         if (!CAUSAL || kb <= q0 + wave_u * 32 + 31) {
+        // every key of the tile is < S and (causal) before every query of the
+        // wave (queries past S only feed dQ rows that are never stored)
+        const bool unmasked = kb + BSTEP <= S && (!CAUSAL || kb + BSTEP - 1 <= q0 + wave_u * 32);
         // S^T = K Q^T, dP^T = V dO^T: 64 keys x this wave's 32 queries
         bf16x8_t sb[2][2];  // dS^T as B operands: [32-key half][16-key step]
 #pragma unroll
@@ -514,14 +534,21 @@ __global__ __launch_bounds__(QT, 2) void flash_bwd_dq_kernel(
                     if constexpr (m & 1) dp = mfma(as_bf16x8(f[0]), of[m >> 1], dp);
                     else s = mfma(as_bf16x8(f[0]), qf[m >> 1], s);
                 });
-            // register r: key kb + h*32 + 8(r/4) + 4g + r%4
+            // register r: key kb + h*32 + 8(r/4) + 4g + r%4; unmasked, then
+            // the last tile and the diagonal zero the masked elements (see
+            // the dK/dV pass)
             float ds[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int k = kb + h * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                const bool live = k < S && q < S && (!CAUSAL || k <= q);
-                const float pv = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -lse2)) : 0.0f;
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -lse2));
                 ds[r] = pv * (dp[r] - dvq);
+            }
+            if (!unmasked) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int k = kb + h * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (!(k < S && q < S && (!CAUSAL || k <= q))) ds[r] = 0.0f * (dp[r] - dvq);
+                }
             }
 #pragma unroll
             for (int t2 = 0; t2 < 2; ++t2) sb[h][t2] = pack8(ds + 8 * t2);
