@@ -151,13 +151,16 @@ __device__ __forceinline__ uint32_t tr_addr(const uint8_t* tile, int rb, int dt,
 struct TrFrag {
     u32x2_t lo, hi;
 };
-template <int D>
+// OFF: a compile-time byte offset added by the instruction itself (one base
+// register per pipeline instead of one address computation per read)
+template <int D, int OFF>
 __device__ __forceinline__ TrFrag tr_issue(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF + 8 * BwdCfg<D>::PITCH < 65536, "16-bit LDS offset");
     TrFrag f;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(f.lo) : "v"(addr) : "memory");
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(f.lo) : "v"(addr), "n"(OFF) : "memory");
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
                  : "=v"(f.hi)
-                 : "v"(addr), "n"(8 * BwdCfg<D>::PITCH)
+                 : "v"(addr), "n"(OFF + 8 * BwdCfg<D>::PITCH)
                  : "memory");
     return f;
 }
@@ -171,25 +174,33 @@ __device__ __forceinline__ bf16x8_t tr_wait(TrFrag& f) {
 // Runs NM MFMAs whose fragments come from transposing reads: the reads of
 // MFMAs m+1 .. m+L are in flight while m runs, in a ring of L+2 fragments
 // (a fragment is refilled only after the MFMA two before has taken it).
-// addr(m) gives MFMA m's read address, use(m, frag) issues MFMA m.
-template <int D, int NM, int L, typename A, typename U>
-__device__ __forceinline__ void tr_pipeline(A&& addr, U&& use) {
+// MFMA m reads at base + off(m), off returning std::integral_constant (a
+// compile-time offset); use(m, frag) issues MFMA m.
+template <int M>
+using ic = std::integral_constant<int, M>;
+template <int D, int NM, int L, typename O, typename U>
+__device__ __forceinline__ void tr_pipeline(uint32_t base, O&& off, U&& use) {
     constexpr int R = L + 2;
     TrFrag ring[R];
-    static_for<0, L>([&](auto mi) { ring[decltype(mi)::value] = tr_issue<D>(addr(decltype(mi)::value)); });
+    static_for<0, L>([&](auto mi) {
+        constexpr int m = decltype(mi)::value;
+        ring[m] = tr_issue<D, decltype(off(ic<m>{}))::value>(base);
+    });
     static_for<0, NM>([&](auto mi) {
         constexpr int m = decltype(mi)::value;
-        if constexpr (m + L < NM) ring[(m + L) % R] = tr_issue<D>(addr(m + L));
+        if constexpr (m + L < NM) ring[(m + L) % R] = tr_issue<D, decltype(off(ic<m + L>{}))::value>(base);
         constexpr int later = (m + L < NM ? L : NM - 1 - m);  // MFMAs whose reads follow m's
         use(mi, tr_wait<2 * later>(ring[m % R]));
     });
 }
 
 // Row fragments (16-byte reads) in the same way: MFMA m takes RPM reads,
-// addr(m, j) is the address of its read j, use(m, frags) issues it.
+// read j at base + off(m, j) (a compile-time offset), use(m, frags) issues it.
+template <int OFF>
 __device__ __forceinline__ u32x4_t b128_issue(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "16-bit LDS offset");
     u32x4_t v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
     return v;
 }
 template <int N>
@@ -200,19 +211,22 @@ template <int N>
 __device__ __forceinline__ void b128_wait(u32x4_t& a, u32x4_t& b) {
     asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
 }
-template <int NM, int RPM, int L, typename A, typename U>
-__device__ __forceinline__ void row_pipeline(A&& addr, U&& use) {
+template <int NM, int RPM, int L, typename O, typename U>
+__device__ __forceinline__ void row_pipeline(uint32_t base, O&& off, U&& use) {
     static_assert(RPM == 1 || RPM == 2, "one or two reads per MFMA");
     constexpr int R = L + 2;
     u32x4_t ring[R][RPM];
-    auto issue = [&](int m, int slot) {
-#pragma unroll
-        for (int j = 0; j < RPM; ++j) ring[slot][j] = b128_issue(addr(m, j));
+    auto issue = [&](auto mi) {
+        constexpr int m = decltype(mi)::value;
+        static_for<0, RPM>([&](auto ji) {
+            constexpr int j = decltype(ji)::value;
+            ring[m % R][j] = b128_issue<decltype(off(ic<m>{}, ic<j>{}))::value>(base);
+        });
     };
-    static_for<0, L>([&](auto mi) { issue(decltype(mi)::value, decltype(mi)::value); });
+    static_for<0, L>([&](auto mi) { issue(mi); });
     static_for<0, NM>([&](auto mi) {
         constexpr int m = decltype(mi)::value;
-        if constexpr (m + L < NM) issue(m + L, (m + L) % R);
+        if constexpr (m + L < NM) issue(ic<m + L>{});
         constexpr int later = (m + L < NM ? L : NM - 1 - m);
         if constexpr (RPM == 1) b128_wait<later>(ring[m % R][0]);
         else b128_wait<2 * later>(ring[m % R][0], ring[m % R][1]);
@@ -402,8 +416,14 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
         // transposed in the matching query order
         // MFMA m = (dt, t, which): which 0 = dV (dO read), 1 = dK (Q read);
         // the reads of MFMAs m+1 and m+2 are in flight while m runs
+        // MFMA m reads rows 16 ((m >> 1) & 1) + .. of Q (odd m) or dO, d block
+        // m >> 2: do_t = q_t + KVSTEP rows, so one base and constant offsets
         tr_pipeline<D, 4 * C::DT, 2>(
-            [&](int m) { return tr_addr<D>((m & 1) ? q_t : do_t, 16 * ((m >> 1) & 1), m >> 2, lane); },
+            tr_addr<D>(q_t, 0, 0, lane),
+            [](auto mi) {
+                constexpr int m = decltype(mi)::value;
+                return ic<((m & 1) ? 0 : KVSTEP * C::PITCH) + 16 * ((m >> 1) & 1) * C::PITCH + 64 * (m >> 2)>{};
+            },
             [&](auto mi, bf16x8_t b) {
                 constexpr int m = decltype(mi)::value, dt = m >> 2, t = (m >> 1) & 1;
                 if constexpr (m & 1) dk[dt] = mfma(sa[0][t], b, dk[dt]);
@@ -527,8 +547,13 @@ __global__ __launch_bounds__(QT, 2) void flash_bwd_dq_kernel(
         for (int h = 0; h < 2; ++h) {
             f32x16_t s = zero16(), dp = zero16();
             // S^T and dP^T MFMAs alternate: m = 2 ks + which
+            // MFMA m reads V (odd m) or K, k-step m >> 1: v_t = k_t + BSTEP rows
             row_pipeline<2 * C::KS, 1, 2>(
-                [&](int m, int) { return row_addr<D>((m & 1) ? v_t : k_t, h * 32 + col, m >> 1, g); },
+                row_addr<D>(k_t, h * 32 + col, 0, g),
+                [](auto mi, auto) {
+                    constexpr int m = decltype(mi)::value;
+                    return ic<((m & 1) ? BSTEP * C::PITCH : 0) + 32 * (m >> 1)>{};
+                },
                 [&](auto mi, u32x4_t* f) {
                     constexpr int m = decltype(mi)::value;
                     if constexpr (m & 1) dp = mfma(as_bf16x8(f[0]), of[m >> 1], dp);
@@ -556,7 +581,11 @@ __global__ __launch_bounds__(QT, 2) void flash_bwd_dq_kernel(
         // dQ^T += K^T dS^T: A = K read transposed in the matching key order
         // MFMA m = (dt, h, t2); the reads of MFMAs m+1 and m+2 are in flight
         tr_pipeline<D, 4 * C::DT, 2>(
-            [&](int m) { return tr_addr<D>(k_t, 16 * (m & 3), m >> 2, lane); },
+            tr_addr<D>(k_t, 0, 0, lane),
+            [](auto mi) {
+                constexpr int m = decltype(mi)::value;
+                return ic<16 * (m & 3) * C::PITCH + 64 * (m >> 2)>{};
+            },
             [&](auto mi, bf16x8_t a) {
                 constexpr int m = decltype(mi)::value, dt = m >> 2, h = (m >> 1) & 1, t2 = m & 1;
                 dq[dt] = mfma(a, sb[h][t2], dq[dt]);
