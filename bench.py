@@ -126,8 +126,8 @@ BWD_CONFIGS = {
 
 # matmulInt8 (FusedKernels.h:867; a hot-path function with no BASELINE
 # config): a square MFMA-tile shape, and the decode shape of C5 with int8
-# activations (the reference benchmark's own matmulInt8 case in SURVEY's
-# CPU-baseline plan), weights rotated through HBM like C5.
+# activations (M=8, N=K=8192, the shape the CPU baseline times matmulInt8
+# at), weights rotated through HBM like C5.
 INT8_CONFIGS = {
     "i1": dict(kind="int8", M=4096, N=4096, K=4096),
     "i2": dict(kind="int8", M=8, N=8192, K=8192),

@@ -7,9 +7,9 @@
 // with the same class names, method names, argument meaning and return types,
 // two substitutions: element types are jh_dtype (jules_hip.h) instead of
 // jules::ScalarType::ScalarKind, and failures throw jules_hip::PJRTError
-// instead of reporting through a DiagnosticsEngine.  INTEGRATION.md shows the
-// adapter that lets the reference's PJRTClient::create("rocm", diag) return
-// this client (today it falls back to the CPU client, PJRT.cpp:1278-1284).
+// instead of reporting through a DiagnosticsEngine.  The reference's
+// PJRTClient::create("rocm", diag) falls back to the CPU client today
+// (PJRT.cpp:1278-1284); an adapter there can return this client instead.
 //
 // Executables take the same program text as the reference's CPU executable
 // (StableHLO in generic op form, `%r = "stablehlo.op"(%a, %b) {...} : ...`)

@@ -187,7 +187,8 @@ def test_gemm_tile_invariance():
 def test_tile_planner_restatement():
     """TilePlanner::computeAnalytical (TilePlanner.h:97-136) with this
     container's cache sizes as the reference reads them (index0 = 48K L1d,
-    index1 = 32K L1i taken as L2): the survey's recorded picks."""
+    index1 = 32K L1i taken as L2): the tiles the reference's planner picks
+    on that machine."""
     assert po.tile_analytical(512, 512, 512) == (32, 32, 128)
     assert po.tile_analytical(8, 8, 8) == (16, 16, 8)
     # K*N*4 fits 3/4 of L2 -> tile_k = K
