@@ -265,6 +265,12 @@ size_t jules_hip_w8a16_noalloc_max_bytes(void);
 int jules_hip_w8a16_gemm_bias_act_noalloc(int act, const void* x, const int8_t* W,
                                           const float* scale, const float* bias,
                                           void* y, int M, int N, int K, void* stream);
+/* Diagnostics for the entry point above (no reference counterpart): copies
+ * the first n (0 <= n <= 1024) per-column-tile arrival counters of the
+ * current GPU's static array into host memory out, after waiting for the
+ * device.  Every call that has finished leaves them all 0; a counter that is
+ * not 0 with no call running means a launch was aborted part-way. */
+int jules_hip_w8a16_noalloc_counters(uint32_t* out, int n);
 
 /* ---- int8 x int8 GEMM (matmulInt8 semantics) -------------------------------
  * C[i,j] = float(sum_k A[i,k]*B[k,j]) * (scale_A*scale_B) [+ bias[j]]

@@ -15,6 +15,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <unordered_map>
 #include <vector>
 
 #include "jules_hip.h"
@@ -49,6 +50,17 @@ struct CacheInfo {
     static CacheInfo detect();
 };
 
+// reference TilePlanner.h:59-72: the key of the planner's per-shape cache
+struct ShapeSignature {
+    int m, n, k;
+    bool operator==(const ShapeSignature& o) const { return m == o.m && n == o.n && k == o.k; }
+    struct Hash {
+        size_t operator()(const ShapeSignature& s) const {
+            return ((size_t)s.m << 32) | ((size_t)s.n << 16) | (size_t)s.k;
+        }
+    };
+};
+
 // reference TilePlanner.h:74-294.  computeAnalytical returns the tile the
 // fp32 GEMM launch uses by default (the library's table); getTileConfig
 // caches per shape and, with auto-tuning on (the default, as in the
@@ -56,25 +68,35 @@ struct CacheInfo {
 // shape on the current GPU (one warm-up and 10 timed launches each, HIP
 // events) and keeps the fastest.  Like the reference, one planner object is
 // not safe to use from two threads at once.
+//
+// setBenchmarkKernel (reference TilePlanner.h:141-148) registers the function
+// that auto-tuning times instead: as in the reference it is called with HOST
+// buffers (A, B filled with 1.0f, C of M*N floats), M, N, K and each
+// candidate TileConfig, one warm-up and 10 timed calls per candidate on the
+// host clock, and must be synchronous.  The candidates stay the GPU table's
+// tiles; a captureless lambda that calls tiledMatmulWithActivation below is a
+// valid registration.
 class TilePlanner {
 public:
+    using BenchmarkKernelFn = void (*)(const float*, const float*, float*, int, int, int,
+                                       const TileConfig&);
     explicit TilePlanner(const CacheInfo& cache = CacheInfo::detect());
     TileConfig getTileConfig(int M, int N, int K);
     TileConfig computeAnalytical(int M, int N, int K) const;
     void setAutoTune(bool enabled) { autoTune_ = enabled; }
     void setVerbose(bool v) { verbose_ = v; }
     const CacheInfo& cacheInfo() const { return cache_; }
+    void setBenchmarkKernel(BenchmarkKernelFn fn) { benchmarkKernel_ = fn; }
 
 private:
     TileConfig autoTune(int M, int N, int K, const TileConfig& defaultConfig);
-    struct Entry {
-        int m, n, k;
-        TileConfig cfg;
-    };
+    TileConfig autoTuneWith(BenchmarkKernelFn fn, int M, int N, int K,
+                            const TileConfig& defaultConfig);
     CacheInfo cache_;
     bool autoTune_ = true;
     bool verbose_ = false;
-    std::vector<Entry> configCache_;
+    BenchmarkKernelFn benchmarkKernel_ = nullptr;
+    std::unordered_map<ShapeSignature, TileConfig, ShapeSignature::Hash> configCache_;
 };
 
 // reference ExecutionArena.h:94-199: bump allocator over one DEVICE buffer
@@ -93,10 +115,24 @@ public:
     void* allocateBytes(size_t bytes);
     void reset() { offset_ = 0; }
     void resetAndZero();
+    // reference ExecutionArena.h:170-187 issues CPU cache-prefetch hints over
+    // [addr, addr + size).  The kernels here stream their operands from HBM
+    // through the GPU's own caches, and a host-side hint would warm the CPU
+    // caches with data the GPU does not read from there, so these do nothing.
+    void prefetch(const void* addr, size_t size, int level = 1) const {
+        (void)addr;
+        (void)size;
+        (void)level;
+    }
+    template <typename T>
+    void prefetchTensor(const T* data, size_t count, int level = 1) const {
+        prefetch(data, count * sizeof(T), level);
+    }
     size_t usedBytes() const { return offset_; }
     size_t highWaterMark() const { return highWaterMark_; }
     size_t capacity() const { return maxSize_; }
     char* rawBuffer() { return buffer_; }
+    const char* rawBuffer() const { return buffer_; }
 
 private:
     char* buffer_ = nullptr;

@@ -54,6 +54,7 @@ SIGNATURES = {
     "jules_hip_w8a16_packed_gemm_bias_act": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _int, _int,
                                                     _int, _vp]),
     "jules_hip_w8a16_noalloc_max_bytes": (_size, []),
+    "jules_hip_w8a16_noalloc_counters": (_int, [_vp, _int]),
     "jules_hip_w8a16_gemm_bias_act_noalloc": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _int, _int,
                                                      _int, _vp]),
     "jules_hip_matmul_int8": (_int, [_vp, _vp, _vp, _int, _int, _int, _f32, _f32, _vp, _vp]),

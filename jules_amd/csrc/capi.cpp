@@ -352,6 +352,21 @@ int jules_hip_w8a16_gemm_bias_act_noalloc(int act, const void* x, const int8_t* 
                      "w8a16 noalloc launch");
 }
 
+int jules_hip_w8a16_noalloc_counters(uint32_t* out, int n) {
+    const int words = 4096 / (int)sizeof(uint32_t);
+    if (n < 0 || n > words) return fail(JH_ERR_ARG, "w8a16 noalloc counters: n=%d (0..%d)", n, words);
+    if (n == 0) return JH_OK;
+    if (!out) return fail(JH_ERR_NULL, "w8a16 noalloc counters: out is NULL");
+    void* ws = nullptr;
+    int st = check_hip(jh::static_scratch(&ws), "w8a16 noalloc counters: scratch address");
+    if (st != JH_OK) return st;
+    st = check_hip(hipDeviceSynchronize(), "w8a16 noalloc counters: device");
+    if (st != JH_OK) return st;
+    return check_hip(hipMemcpy(out, static_cast<char*>(ws) + jh::static_scratch_partial_bytes(),
+                               sizeof(uint32_t) * (size_t)n, hipMemcpyDeviceToHost),
+                     "w8a16 noalloc counters: copy");
+}
+
 int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M, int N, int K,
                           float scale_A, float scale_B, const float* bias, void* stream) {
     if (M < 0 || N < 0 || K < 0) return fail(JH_ERR_SHAPE, "matmulInt8: M=%d N=%d K=%d", M, N, K);

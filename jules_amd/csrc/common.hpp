@@ -2,8 +2,12 @@
 //
 // Every translation unit of the library is compiled with -ffp-contract=off:
 // the activation helpers below perform the same IEEE-754 operations in the
-// same order as the reference's AVX-512 helpers, so a multiply and an add must
-// not be fused unless written as an fma.
+// same order as the reference's AVX-512 helpers as g++ compiles them, so a
+// multiply and an add are fused exactly where written as an fma.  Those fmas
+// include the ones g++ makes at its default -ffp-contract=fast: it expands
+// _mm512_add/sub/mul_ps into generic vector arithmetic and fuses a product
+// into the adds and subtracts that consume it when those are its only uses
+// (marked "contracted" below).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -24,10 +28,13 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // ---- activation epilogue ---------------------------------------------------
 
-// fast_exp_zmm of reference FusedKernels.h:90-133, one lane: clamp to
-// [-88,88], r = x*log2(e), floor split, degree-6 Horner in fma, 2^floor from
-// exponent bits, product.
-__device__ __forceinline__ float fast_exp(float x) {
+// fast_exp_zmm of reference FusedKernels.h:90-133, one lane, as its two
+// factors: clamp to [-88,88], r = x*log2(e), floor split, degree-6 Horner in
+// fma, 2^floor from exponent bits.  The result is scale*poly.
+struct ExpParts {
+    float scale, poly;
+};
+__device__ __forceinline__ ExpParts fast_exp_parts(float x) {
     x = (x < 88.0f) ? x : 88.0f;
     x = (x > -88.0f) ? x : -88.0f;
     const float r = x * 1.4426950408889634f;
@@ -40,25 +47,32 @@ __device__ __forceinline__ float fast_exp(float x) {
     p = __builtin_fmaf(p, rf, 0.693147180f);
     p = __builtin_fmaf(p, rf, 1.0f);
     const int e = ((int)ri + 127) << 23;
-    return __int_as_float(e) * p;
+    return ExpParts{__int_as_float(e), p};
 }
 
-// fast_tanh_zmm, reference FusedKernels.h:137-143
+__device__ __forceinline__ float fast_exp(float x) {
+    const ExpParts e = fast_exp_parts(x);
+    return e.scale * e.poly;
+}
+
+// fast_tanh_zmm, reference FusedKernels.h:137-143: (e-1)/(e+1) with
+// e = exp(2x); both the subtract and the add are contracted.
 __device__ __forceinline__ float fast_tanh(float x) {
-    const float e = fast_exp(2.0f * x);
-    return __fdiv_rn(e - 1.0f, e + 1.0f);
+    const ExpParts e = fast_exp_parts(2.0f * x);
+    return __fdiv_rn(__builtin_fmaf(e.scale, e.poly, -1.0f), __builtin_fmaf(e.scale, e.poly, 1.0f));
 }
 
-// sigmoid_zmm, reference FusedKernels.h:146-152
+// sigmoid_zmm, reference FusedKernels.h:146-152: 1/(1+exp(0-x)), the add
+// contracted
 __device__ __forceinline__ float sigmoid(float x) {
-    const float e = fast_exp(0.0f - x);
-    return __fdiv_rn(1.0f, 1.0f + e);
+    const ExpParts e = fast_exp_parts(0.0f - x);
+    return __fdiv_rn(1.0f, __builtin_fmaf(e.scale, e.poly, 1.0f));
 }
 
-// gelu_zmm, reference FusedKernels.h:155-164
+// gelu_zmm, reference FusedKernels.h:155-164; x + 0.044715*x^3 contracted
 __device__ __forceinline__ float gelu(float x) {
     const float x3 = x * (x * x);
-    const float inner = 0.7978845608f * (x + 0.044715f * x3);
+    const float inner = 0.7978845608f * __builtin_fmaf(0.044715f, x3, x);
     const float t = fast_tanh(inner);
     return 0.5f * (x * (1.0f + t));
 }

@@ -224,15 +224,15 @@ __global__ void activation_kernel(float* out, const float* __restrict__ in, int6
 
 // fusedGelu (reference FusedKernels.h:606-627): gelu_zmm on the full groups
 // of 16 elements, and on the last partial group (the n % 16 elements from
-// n & ~15 on) the scalar formula with libm tanhf and x*x*x evaluated left to
-// right, as the reference's tail loop does.
+// n & ~15 on) the scalar formula with tanhf, evaluated left to right as the
+// reference's tail loop is compiled: x + (0.044715*x*x)*x is one fma.
 __global__ void fused_gelu_kernel(float* out, const float* __restrict__ in, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int64_t nv = n & ~int64_t(15);
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
         const float x = in[i];
         out[i] = i < nv ? gelu(x)
-                        : 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+                        : 0.5f * x * (1.0f + tanhf(0.7978845608f * __builtin_fmaf(0.044715f * x * x, x, x)));
     }
 }
 

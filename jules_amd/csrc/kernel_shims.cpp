@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -15,6 +16,10 @@
 #include "jules_hip_kernel.hpp"
 #include "launch.hpp"
 #include "tiles.hpp"
+
+namespace jh {
+int set_last_error(int status, const std::string& message);  // capi.cpp
+}
 
 namespace jules {
 namespace kernel {
@@ -157,12 +162,43 @@ TileConfig TilePlanner::computeAnalytical(int M, int N, int K) const {
 }
 
 TileConfig TilePlanner::getTileConfig(int M, int N, int K) {
-    for (const Entry& e : configCache_)
-        if (e.m == M && e.n == N && e.k == K) return e.cfg;
+    const ShapeSignature sig{M, N, K};
+    auto it = configCache_.find(sig);
+    if (it != configCache_.end()) return it->second;
     TileConfig cfg = computeAnalytical(M, N, K);
-    if (autoTune_ && M >= 32 && N >= 32) cfg = autoTune(M, N, K, cfg);  // TilePlanner.h:88-90
-    configCache_.push_back(Entry{M, N, K, cfg});
+    if (autoTune_ && M >= 32 && N >= 32)  // TilePlanner.h:88-90
+        cfg = benchmarkKernel_ ? autoTuneWith(benchmarkKernel_, M, N, K, cfg)
+                               : autoTune(M, N, K, cfg);
+    configCache_[sig] = cfg;
     return cfg;
+}
+
+// The registered benchmark function over the table's tiles for this depth,
+// on host buffers of ones (TilePlanner.h:188-236), host-clock timed.
+TileConfig TilePlanner::autoTuneWith(BenchmarkKernelFn fn, int M, int N, int K,
+                                     const TileConfig& defaultConfig) {
+    std::vector<float> A((size_t)M * K, 1.0f), B((size_t)K * N, 1.0f), C((size_t)M * N, 0.0f);
+    TileConfig best = defaultConfig;
+    double best_ms = 1e18;
+    for (int v = jh::GV_F32_ROWS1; v <= jh::GV_F32_T64; ++v) {
+        if (!jh::f32_variant_valid(v, K)) continue;
+        const TileConfig cfg = to_config(jh::f32_variant_tile(v, K));
+        fn(A.data(), B.data(), C.data(), M, N, K, cfg);  // warm-up, not timed
+        constexpr int iters = 10;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; ++i) fn(A.data(), B.data(), C.data(), M, N, K, cfg);
+        const double ms =
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() /
+            iters;
+        if (ms < best_ms) {
+            best_ms = ms;
+            best = cfg;
+        }
+    }
+    if (verbose_)
+        std::printf("Auto-tune [%d,%d]x[%d,%d]: tile=(%d,%d,%d) %.3fms\n", M, K, K, N, best.tile_m,
+                    best.tile_n, best.tile_k, best_ms);
+    return best;
 }
 
 // Times each table kernel that can run the shape (TilePlanner.h:158-236 does
@@ -253,6 +289,26 @@ void fusedMatmulBiasRelu(const float* X, const float* W, const float* bias, floa
 
 void tiledMatmulWithActivation(const float* A, const float* B, float* C, int M, int N, int K,
                                const TileConfig& cfg, ActivationType act) {
+    if (K == 0 && M > 0 && N > 0) {
+        // The reference zeroes C (FusedKernels.h:382) and applies the
+        // activation only inside its K-slice loop (:407), which K = 0 never
+        // enters: C stays 0 for every activation (act(0) is 0.5 for sigmoid).
+        const size_t bytes = sizeof(float) * (size_t)M * (size_t)N;
+        int st = JH_OK;
+        if (is_device_ptr(C)) {
+            if (hipMemset(C, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+                st = JH_ERR_HIP;
+        } else if (C) {
+            std::memset(C, 0, bytes);
+        } else {
+            st = JH_ERR_NULL;
+        }
+        if (st == JH_ERR_HIP) (void)hipGetLastError();
+        if (st != JH_OK)
+            jh::set_last_error(st, st == JH_ERR_NULL ? "tiledMatmulWithActivation: C is null"
+                                                     : "tiledMatmulWithActivation: zeroing C failed");
+        return record(st);
+    }
     run_gemm(A, B, nullptr, C, M, N, K, static_cast<int>(act), variant_of(cfg, K));
 }
 

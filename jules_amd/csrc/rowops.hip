@@ -410,11 +410,12 @@ __global__ __launch_bounds__(RT) void cross_entropy_reduce_kernel(const float* _
                                                                   float* __restrict__ loss, int M) {
     __shared__ float part[RT / 64];
     float s = 0.0f;
-    for (int i0 = threadIdx.x; i0 < M; i0 += RT * RU) {
+    // 64-bit row indices: i0 + RT * u would overflow int for M near INT_MAX
+    for (int64_t i0 = threadIdx.x; i0 < M; i0 += RT * RU) {
         float v[RU];
 #pragma unroll
         for (int u = 0; u < RU; ++u) {
-            const int i = i0 + RT * u;
+            const int64_t i = i0 + (int64_t)RT * u;
             v[u] = i < M ? row_loss[i] : 0.0f;
         }
 #pragma unroll

@@ -243,10 +243,14 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     // call_id is new for every call, so flags from earlier calls or
     // uninitialised workspace never match.
     // Counter protocol (COUNTER): after its partial stores complete, wave 0
-    // adds 1 to counters[tile] (agent-scope atomic with return); the
-    // workgroup that receives KS-1 is the tile's last arrival, resets the
-    // counter to 0 for the next call and reduces.  Exactly one workgroup
-    // reduces.
+    // increments counters[tile] with a wrapping atomic (global_atomic_inc
+    // with limit KS-1: old == KS-1 stores 0, otherwise old+1, one agent-scope
+    // read-modify-write); the workgroup that receives KS-1 is the tile's last
+    // arrival and reduces, and its own increment has already put the counter
+    // back to 0 for the next call.  Exactly one workgroup reduces.  Because
+    // the reset is part of the atomic, an increment of an overlapping call
+    // is never lost: once every call that ran has finished, each counter has
+    // taken a multiple of KS increments and is 0 again.
     const int tiles = gridDim.x;
     {
         const __amdgpu_buffer_rsrc_t pr = part_rsrc(partials, split, tiles, tile, true);
@@ -262,11 +266,9 @@ __global__ __launch_bounds__(THREADS, 1) void w8a16_splitk_kernel(
     lds_barrier();                        // ... and every wave's
     if constexpr (COUNTER) {
         if (wave == 0 && lane == 0) {
-            const uint32_t old =
-                __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const bool is_last = old == (uint32_t)(KS - 1);
-            if (is_last) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = is_last;
+            const uint32_t old = __builtin_amdgcn_atomic_inc32(counters + tile, (uint32_t)(KS - 1),
+                                                               __ATOMIC_RELAXED, "agent");
+            last = old == (uint32_t)(KS - 1);
         }
     } else if (wave == 0) {
         uint64_t* tf = flags + (int64_t)tile * KS;

@@ -9,9 +9,17 @@
  * hot loops carry target_clones so one .so built here runs on any x86-64 host
  * and still uses 512-bit FMA where the host has AVX-512F.
  *
- * -ffp-contract=off matters: the reference's vector path issues every
- * multiply, add and fma as a separate intrinsic, so the restatement must not
- * let the compiler fuse a multiply and an add that the reference keeps apart.
+ * -ffp-contract=off matters: the restatement spells out every fma the
+ * reference's compiled code performs and nothing else.  Those fmas are more
+ * than the reference's explicit _mm512_fmadd_ps calls: g++ (11.4, the image's
+ * compiler, C++ at its default -ffp-contract=fast, the flags of
+ * benchmarks/bench_kernel.cpp:15-19 plus -mavx512bw) expands _mm512_add_ps,
+ * _mm512_sub_ps and _mm512_mul_ps into generic vector arithmetic and then
+ * fuses a product into every add or subtract that consumes it, when every use
+ * of the product is one.  The places where that happens on this path are
+ * marked "contracted" below; tests/cpp/gxx_activation_probe.cpp compiles the
+ * intrinsic sequences with those flags and tests/test_oracle.py checks the
+ * restatement against its output bit for bit.
  */
 #include "jules_oracle.h"
 
@@ -32,15 +40,16 @@ static inline int imin(int a, int b) { return a < b ? a : b; }
 /* Activation helpers                                                        */
 /* ------------------------------------------------------------------------ */
 
-/* fast_exp_zmm, reference FusedKernels.h:90-133, one lane.
- * clamp to [-88,88] (:92-95; min/max return the bound for NaN like minps/maxps
- * with the bound as second operand) -> r = x*log2(e) (:98-99) -> floor split
- * (:102-104) -> degree-6 Horner in fma (:109-123) -> 2^floor built from
- * exponent bits (:127-130) -> product (:132). */
-float jo_fast_exp(float x) {
+/* fast_exp_zmm, reference FusedKernels.h:90-133, one lane, as its two
+ * factors: clamp to [-88,88] (:92-95; min/max return the bound for NaN like
+ * minps/maxps with the bound as second operand) -> r = x*log2(e) (:98-99) ->
+ * floor split (:102-104) -> degree-6 Horner in fma (:109-123) -> 2^floor built
+ * from exponent bits (:127-130).  The result is their product (:132); a caller
+ * that only adds or subtracts that product gets it fused instead. */
+static inline void fast_exp_parts(float x, float* scale, float* poly) {
     x = (x < 88.0f) ? x : 88.0f;   /* _mm512_min_ps(x, 88): NaN -> 88 */
     x = (x > -88.0f) ? x : -88.0f; /* _mm512_max_ps(x, -88) */
-    const float r = x * 1.4426950408889634f;
+    const float r = x * 1.4426950408889634f; /* r also feeds the floor: not fused */
     const float ri = floorf(r);
     const float rf = r - ri;
     float p = fmaf(0.000154040f, rf, 0.001333356f);
@@ -50,26 +59,39 @@ float jo_fast_exp(float x) {
     p = fmaf(p, rf, 0.693147180f);
     p = fmaf(p, rf, 1.0f);
     const int32_t e = ((int32_t)ri + 127) << 23; /* cvttps, add 127, shift 23 */
-    return bits_to_float((uint32_t)e) * p;
+    *scale = bits_to_float((uint32_t)e);
+    *poly = p;
 }
 
-/* fast_tanh_zmm, reference FusedKernels.h:137-143: (e^{2x}-1)/(e^{2x}+1) */
+float jo_fast_exp(float x) {
+    float s, p;
+    fast_exp_parts(x, &s, &p);
+    return s * p;
+}
+
+/* fast_tanh_zmm, reference FusedKernels.h:137-143: (e^{2x}-1)/(e^{2x}+1).
+ * e = scale*poly is used only by the subtract and the add, so both are
+ * contracted: (fma(s,p,-1)) / (fma(s,p,1)). */
 float jo_fast_tanh(float x) {
-    const float e = jo_fast_exp(2.0f * x);
-    return (e - 1.0f) / (e + 1.0f);
+    float s, p;
+    fast_exp_parts(2.0f * x, &s, &p);
+    return fmaf(s, p, -1.0f) / fmaf(s, p, 1.0f);
 }
 
-/* sigmoid_zmm, reference FusedKernels.h:146-152: 1/(1+exp(0-x)) */
+/* sigmoid_zmm, reference FusedKernels.h:146-152: 1/(1+exp(0-x)); the add is
+ * contracted: 1/fma(s,p,1). */
 float jo_sigmoid(float x) {
-    const float e = jo_fast_exp(0.0f - x);
-    return 1.0f / (1.0f + e);
+    float s, p;
+    fast_exp_parts(0.0f - x, &s, &p);
+    return 1.0f / fmaf(s, p, 1.0f);
 }
 
 /* gelu_zmm, reference FusedKernels.h:155-164:
- * 0.5*(x*(1+tanh(c*(x + d*(x*(x*x)))))) with c=0.7978845608, d=0.044715 */
+ * 0.5*(x*(1+tanh(c*(x + d*(x*(x*x)))))) with c=0.7978845608, d=0.044715;
+ * x + d*x3 is contracted to fma(d, x3, x). */
 float jo_gelu(float x) {
     const float x3 = x * (x * x);
-    const float inner = 0.7978845608f * (x + 0.044715f * x3);
+    const float inner = 0.7978845608f * fmaf(0.044715f, x3, x);
     const float t = jo_fast_tanh(inner);
     return 0.5f * (x * (1.0f + t));
 }
@@ -90,13 +112,20 @@ float jo_act(int act, float x) {
     }
 }
 
+/* The scalar GELU formula of the reference's tails (FusedKernels.h:426,
+ * :616): 0.5f*x*(1+tanhf(c*(x + 0.044715f*x*x*x))), evaluated left to right,
+ * with x + (0.044715f*x*x)*x contracted to one fma. */
+static inline float gelu_tail(float x) {
+    return 0.5f * x * (1.0f + tanhf(0.7978845608f * fmaf(0.044715f * x * x, x, x)));
+}
+
 /* Scalar-tail epilogue, reference FusedKernels.h:424-430 (columns past the
  * last full 16-wide vector of a tile): libm tanhf/expf and std::max. */
 float jo_act_tail(int act, float s) {
     switch (act) {
     case JO_ACT_RELU: return (s < 0.0f) ? 0.0f : s; /* std::max(s, 0.0f) */
     case JO_ACT_GELU:
-        return 0.5f * s * (1.0f + tanhf(0.7978845608f * (s + 0.044715f * s * s * s)));
+        return gelu_tail(s);
     case JO_ACT_SIGMOID: return 1.0f / (1.0f + expf(-s));
     case JO_ACT_TANH: return tanhf(s);
     case JO_ACT_SILU: return s / (1.0f + expf(-s));
@@ -122,10 +151,7 @@ void jo_fused_gelu(float* out, const float* in, int n) {
         if (i + 15 < n) {
             for (int l = 0; l < 16; l++) out[i + l] = jo_gelu(in[i + l]);
         } else {
-            for (int j = i; j < n; j++) {
-                const float x = in[j];
-                out[j] = 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
-            }
+            for (int j = i; j < n; j++) out[j] = gelu_tail(in[j]);
         }
     }
 }

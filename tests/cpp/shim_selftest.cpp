@@ -144,6 +144,26 @@ int main(int argc, char** argv) {
     CHECK(in_table);
     const TileConfig tc2 = tuned.getTileConfig(GM, GN, GK);  // cached
     CHECK(tc2.tile_m == tc.tile_m && tc2.tile_n == tc.tile_n && tc2.tile_k == tc.tile_k);
+    // a registered benchmark function is what auto-tuning times
+    // (TilePlanner.h:141-148): it sees host buffers of ones and table tiles
+    step("setBenchmarkKernel");
+    static int bench_calls = 0;
+    static bool bench_ok = true;
+    TilePlanner custom;
+    custom.setBenchmarkKernel([](const float* a, const float* b, float* c, int m, int n, int k,
+                                 const TileConfig& cfg) {
+        ++bench_calls;
+        bench_ok &= a[0] == 1.0f && b[(size_t)k * n - 1] == 1.0f;
+        tiledMatmulWithActivation(a, b, c, m, n, k, cfg, ActivationType::Relu);
+        bench_ok &= lastStatus() == JH_OK && c[0] == (float)k;
+    });
+    const TileConfig tb = custom.getTileConfig(GM, GN, GK);
+    ok_status("setBenchmarkKernel");
+    CHECK(bench_ok && bench_calls >= 2 * 11);  // >= 2 candidates, 1 warm-up + 10 timed each
+    bool tb_in_table = false;
+    for (const TileConfig& c : table)
+        tb_in_table |= c.tile_m == tb.tile_m && c.tile_n == tb.tile_n && c.tile_k == tb.tile_k;
+    CHECK(tb_in_table);
 
     // ---- GEMM shims --------------------------------------------------------
     std::vector<float> out(GM * GN);
@@ -158,6 +178,25 @@ int main(int argc, char** argv) {
         tiledMatmulWithActivation(dA, dB, dC, GM, GN, GK, tc, static_cast<ActivationType>(act));
         ok_status(n.c_str());
         save(n + "_D", from_dev(dC, out.size()));
+    }
+    // K = 0: the reference zeroes C and applies the activation only inside
+    // its K-slice loop (FusedKernels.h:382,407), so C stays 0 even for
+    // sigmoid, whose act(0) is 0.5; host and device buffers
+    step("tiled K=0");
+    {
+        std::vector<float> k0(GM * GN, 7.0f);
+        tiledMatmulWithActivation(A.data(), B.data(), k0.data(), GM, GN, 0, tc,
+                                  ActivationType::Sigmoid);
+        ok_status("tiled K=0 host");
+        bool zero = true;
+        for (float v : k0) zero &= v == 0.0f && !std::signbit(v);
+        CHECK(zero);
+        float* dk0 = to_dev(std::vector<float>(GM * GN, 7.0f));
+        tiledMatmulWithActivation(dA, dB, dk0, GM, GN, 0, tc, ActivationType::Sigmoid);
+        ok_status("tiled K=0 device");
+        zero = true;
+        for (float v : from_dev(dk0, (size_t)GM * GN)) zero &= v == 0.0f;
+        CHECK(zero);
     }
     for (int i = 0; i < 4; ++i) {  // every kernel of the table: same bits
         const std::string n = "gemm_var" + std::to_string(i);

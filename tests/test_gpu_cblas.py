@@ -67,11 +67,13 @@ def _op(X, rows, cols, ld, trans):
 @pytest.mark.parametrize("ta,tb", [(NoTrans, NoTrans), (Trans, NoTrans), (NoTrans, ConjTrans),
                                    (Trans, Trans)])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.75, -1.25), (0.0, 2.0)])
-def test_general_forms(cblas, order, ta, tb, alpha, beta):
+@pytest.mark.parametrize("M,N,K", [(45, 37, 29), (64, 64, 4096)])
+def test_general_forms(cblas, order, ta, tb, alpha, beta, M, N, K):
     """alpha/beta, transposes and both storage orders with padded leading
-    dimensions, against fp64; C's padding is untouched."""
-    M, N, K = 45, 37, 29
-    case(f"cblas_sgemm order={order} ta={ta} tb={tb} alpha={alpha} beta={beta}")
+    dimensions, against fp64; C's padding is untouched.  64 x 64 x 4096 is
+    one output tile, so the library splits K across workgroups and applies
+    alpha, beta (reading C) and the transposes in its split-K reduction."""
+    case(f"cblas_sgemm {M}x{N}x{K} order={order} ta={ta} tb={tb} alpha={alpha} beta={beta}")
     tA, tB = ta != NoTrans, tb != NoTrans
     if order == RowMajor:
         ar, ac = (K, M) if tA else (M, K)

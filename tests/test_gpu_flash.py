@@ -97,6 +97,18 @@ def test_c4_full_size_bf16(dev):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,S,D", [(3, 8, 300, 128), (1, 24, 257, 64)])
+def test_odd_heads_per_xcd_against_fp64(dev, dt, causal, B, H, S, D):
+    """B*H = 24: three heads per XCD in the head-pair workgroup order (one
+    pair incomplete)."""
+    case(f"flash {dt} odd J causal={causal} [{B},{H},{S},{D}]")
+    Q, K, V = I.attn_inputs(B, H, S, D, dt, seed=B * H + S)
+    y = to_np(_run(dev, Q, K, V, dt, causal))
+    assert I.rel_err(y, po.attention64(Q, K, V, causal, ops.default_scale(D))) < I.TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_invariants(dev, dt):
     case(f"flash {dt} invariants")
     B, H, S, D = 1, 2, 160, 128

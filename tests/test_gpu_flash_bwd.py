@@ -69,6 +69,50 @@ def test_large_causal_against_torch_fp32(dev):
         assert err < TOL, f"{name}: rel err {err:.3g}"
 
 
+@pytest.mark.parametrize("B,H,S,D", [(3, 8, 256, 128), (1, 24, 130, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_odd_heads_per_xcd_against_fp64(dev, B, H, S, D, causal):
+    """B*H = 24: three heads per XCD in the head-pair workgroup order, so one
+    pair is incomplete (the mapping's odd case)."""
+    case(f"flash bwd odd J B{B} H{H} S{S} D{D} causal={causal}")
+    Q, K, V, dO = _inputs(B, H, S, D, seed=B * H + S)
+    scale = 1.0 / np.sqrt(D)
+    got = _grads(dev, Q, K, V, dO, causal, scale)
+    ref = po.attention_bwd64(Q, K, V, dO, causal, scale)
+    for name, g, r in zip(("dQ", "dK", "dV"), got, ref):
+        err = I.rel_err(to_np(g), r)
+        assert err < TOL, f"{name}: rel err {err:.3g}"
+
+
+def test_c4_length_causal_against_torch_fp32(dev):
+    """[2, 8, 4096, 128] causal: the sequence length and head-pair mapping of
+    the timed C4-shape backward (16 heads, two per XCD).  Four heads spread
+    over both batches and both members of a pair, against torch fp32 autograd
+    on the GPU, per head (fp32 math; the same bf16 inputs)."""
+    B, H, S, D = 2, 8, 4096, 128
+    case(f"flash bwd [{B},{H},{S},{D}] causal vs torch fp32")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    tq, tk, tv, tdo = (torch.randn((B, H, S, D), generator=g, device=dev).bfloat16()
+                       for _ in range(4))
+    scale = 1.0 / np.sqrt(D)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    O = ops.flash_attention(tq, tk, tv, True, scale, lse=lse)
+    dQ, dK, dV = ops.flash_attention_bwd(tq, tk, tv, O, tdo, lse, True, scale)
+    torch.cuda.synchronize()
+    mask = torch.ones((S, S), dtype=torch.bool, device=dev).triu(1)
+    for b, h in ((0, 0), (0, 5), (1, 2), (1, 7)):
+        q, k, v = (t[b, h].float().requires_grad_(True) for t in (tq, tk, tv))
+        s = torch.matmul(q, k.t().contiguous()) * scale
+        s = s.masked_fill(mask, float("-inf"))
+        o = torch.matmul(torch.softmax(s, dim=-1), v)
+        (o * tdo[b, h].float()).sum().backward()
+        for name, got, ref in (("dQ", dQ, q.grad), ("dK", dK, k.grad), ("dV", dV, v.grad)):
+            err = ((got[b, h].float() - ref).abs().max() / ref.abs().max()).item()
+            assert err < TOL, f"({b},{h}) {name}: rel err {err:.3g}"
+        del q, k, v, s, o
+
+
 def test_deterministic(dev):
     case("flash bwd determinism")
     Q, K, V, dO = _inputs(2, 2, 300, 128, seed=11)

@@ -1,0 +1,92 @@
+"""GPU parity of every GEMM name of the extern_kernel registry, called the way
+the reference's KernelRoutingPass routes them (jules_hip_lookup, descriptor
+ABI): fusedMatmul{,Relu,Sigmoid,Tanh,Gelu} (KernelRoutingPass.cpp:144-166,
+KernelRoutingPass.h:13-23) and fusedMatmulBias{,Relu,Sigmoid,Tanh,Gelu,Silu}
+(KernelRoutingPass.cpp:189-211; fusedMatmulBiasGelu is the routed name of
+BASELINE configs 1 and 3).
+
+fp32 descriptors: bit-exact against the restated reference kernel (one fma
+chain per output from 0, the bias add, the vector-path activation) at C1's
+512^3 and at a ragged shape.  bf16 descriptors: within 1e-2 of the fp64
+oracle, at 264 x 520 x 136 for every name and at C3's full 4096^3 for
+fusedMatmulBiasGelu (sampled rows against fp64, the whole output against a
+torch fp32 product on the GPU)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import inputs as I
+from oracle import pyoracle as po
+from tests.helpers import case, registry_call, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+NAMES = [("fusedMatmul", "none", False), ("fusedMatmulRelu", "relu", False),
+         ("fusedMatmulSigmoid", "sigmoid", False), ("fusedMatmulTanh", "tanh", False),
+         ("fusedMatmulGelu", "gelu", False), ("fusedMatmulBias", "none", True),
+         ("fusedMatmulBiasRelu", "relu", True), ("fusedMatmulBiasSigmoid", "sigmoid", True),
+         ("fusedMatmulBiasTanh", "tanh", True), ("fusedMatmulBiasGelu", "gelu", True),
+         ("fusedMatmulBiasSilu", "silu", True)]
+
+
+def _call(dev, name, with_bias, A, B, bias, dtype):
+    a, b = to_dev(A, dtype, dev), to_dev(B, dtype, dev)
+    c = torch.full((A.shape[0], B.shape[1]), float("nan"), dtype=dtype, device=dev)
+    ins = [a, b] + ([to_dev(bias, torch.float32, dev)] if with_bias else [])
+    st = registry_call(name, ins, [c])
+    assert st == 0, (name, st)
+    torch.cuda.synchronize()
+    return c
+
+
+def test_all_gemm_names_registered():
+    from jules_amd import _lib
+    names = set(_lib.kernel_names())
+    for name, _, _ in NAMES:
+        assert name in names and _lib.lookup(name) is not None, name
+
+
+@pytest.mark.parametrize("name,act,with_bias", NAMES)
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (37, 144, 77)])
+def test_f32_descriptor_bit_exact(dev, name, act, with_bias, M, N, K):
+    case(f"registry {name} f32 {M}x{N}x{K}")
+    A, B, bias = I.gemm_inputs(M, N, K, "f32", seed=M + K)
+    y = to_np(_call(dev, name, with_bias, A, B, bias, torch.float32))
+    np.testing.assert_array_equal(y, po.matmul_bias_act(A, B, bias if with_bias else None, act))
+    tol = 1.5e-5 if act == "tanh" else I.TOL["f32"]  # the reference's own fast_tanh error
+    assert I.rel_err(y, po.gemm64(A, B, bias if with_bias else None, act)) < tol
+
+
+@pytest.mark.parametrize("name,act,with_bias", NAMES)
+def test_bf16_descriptor_against_fp64(dev, name, act, with_bias):
+    M, N, K = 264, 520, 136
+    case(f"registry {name} bf16 {M}x{N}x{K}")
+    A, B, bias = I.gemm_inputs(M, N, K, "bf16", seed=5)
+    y = to_np(_call(dev, name, with_bias, A, B, bias, torch.bfloat16))
+    assert I.rel_err(y, po.gemm64(A, B, bias if with_bias else None, act)) < I.TOL["bf16"]
+
+
+def test_bf16_fused_matmul_bias_gelu_c3(dev):
+    """BASELINE config 3 through its routed name at full size."""
+    M = N = K = 4096
+    case("registry fusedMatmulBiasGelu bf16 4096^3")
+    A, B, bias = I.gemm_inputs(M, N, K, "bf16", seed=0)
+    y = _call(dev, "fusedMatmulBiasGelu", True, A, B, bias, torch.bfloat16)
+    rows = np.unique(np.concatenate([np.arange(0, M, 61), [M - 1]]))[:64].astype(np.int32)
+    o = po.gemm64(A, B, bias, "gelu", rows=rows)
+    assert I.rel_err(to_np(y)[rows], o) < I.TOL["bf16"]
+    a, b = to_dev(A, torch.bfloat16, dev), to_dev(B, torch.bfloat16, dev)
+    t = torch.nn.functional.gelu(a.float() @ b.float() + to_dev(bias, torch.float32, dev),
+                                 approximate="tanh")
+    assert ((y.float() - t).abs().max() / t.abs().max()).item() < I.TOL["bf16"]
+
+
+def test_f32_fused_matmul_bias_gelu_c1_equals_c_abi(dev):
+    """BASELINE config 1 through its routed name gives the C ABI's bits."""
+    from jules_amd import ops
+    case("registry fusedMatmulBiasGelu f32 512^3 vs C ABI")
+    A, B, bias = I.gemm_inputs(512, 512, 512, "f32", seed=0)
+    y = _call(dev, "fusedMatmulBiasGelu", True, A, B, bias, torch.float32)
+    z = ops.gemm_bias_act(to_dev(A, torch.float32, dev), to_dev(B, torch.float32, dev),
+                          to_dev(bias, torch.float32, dev), "gelu")
+    assert torch.equal(y, z)

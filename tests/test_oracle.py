@@ -9,6 +9,10 @@ Q = 0, causal row 0, permutation and tiling invariance) and exact brute force
 plausible slip in the restatement (dropped term, wrong coefficient, transposed
 operand, wrong mask) fails it.
 """
+import ctypes
+import os
+import shutil
+import subprocess
 from fractions import Fraction
 
 import numpy as np
@@ -96,6 +100,112 @@ def test_activation_against_fp64(act):
         assert g[1] == np.float32(20.0) and abs(g[0]) < 1e-6
 
 
+# ---- the reference's bits as g++ compiles them ------------------------------
+_PROBE_SRC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "gxx_activation_probe.cpp")
+_PROBE_LIB = os.path.join(os.path.dirname(_PROBE_SRC), "libgxx_activation_probe.so")
+# benchmarks/bench_kernel.cpp:15-19, plus -mavx512bw (GCC 11's headers need
+# it); no -ffp-contract option, so C++'s default (fast) applies
+_REF_FLAGS = ["-O3", "-mavx512f", "-mavx512dq", "-mavx512vl", "-mfma", "-mavx512bw"]
+
+
+@pytest.fixture(scope="module")
+def gxx_probe():
+    """tests/cpp/gxx_activation_probe.cpp built with the reference's flags:
+    the reference's intrinsic sequences as g++ compiles them."""
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    if (not os.path.exists(_PROBE_LIB)
+            or os.path.getmtime(_PROBE_LIB) < os.path.getmtime(_PROBE_SRC)):
+        tmp = _PROBE_LIB + ".tmp"
+        subprocess.run(["g++", *_REF_FLAGS, "-fPIC", "-shared", _PROBE_SRC, "-o", tmp], check=True)
+        os.replace(tmp, _PROBE_LIB)
+    lib = ctypes.CDLL(_PROBE_LIB)
+    if not lib.probe_has_avx512f():
+        pytest.skip("host CPU has no AVX-512F")
+    f = ctypes.POINTER(ctypes.c_float)
+    lib.probe_act.argtypes = [ctypes.c_int, f, f, ctypes.c_int64]
+    lib.probe_fused_gelu.argtypes = [f, f, ctypes.c_int]
+    lib.probe_tiled.argtypes = [f, f, f] + [ctypes.c_int] * 7
+    return lib
+
+
+def _fp(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _act_inputs():
+    """Every 97th fp32 bit pattern below |x| = 30, plus edge values."""
+    top = np.float32(30.0).view(np.uint32)
+    pos = np.arange(0, top, 97, dtype=np.uint32).view(np.float32)
+    x = np.concatenate([pos, -pos, np.float32([88.0, -88.0, 1e30, -1e30, np.inf, -np.inf])])
+    return np.ascontiguousarray(x[: x.size // 16 * 16])
+
+
+@pytest.mark.parametrize("act", ["relu", "sigmoid", "tanh", "gelu"])
+def test_vector_activation_matches_gxx_build(gxx_probe, act):
+    """The restated vector-path activation equals the reference's intrinsic
+    sequence compiled by g++ with the reference's flags, bit for bit, over
+    ~21M inputs.  g++ fuses x + d*x^3 (gelu) and the add/subtract of
+    exp = scale*poly (tanh, sigmoid) into fmas; a restatement that rounds
+    those products separately fails (checked below for gelu)."""
+    x = _act_inputs()
+    want = np.empty_like(x)
+    gxx_probe.probe_act(po.ACT[act], _fp(want), _fp(x), x.size)
+    got = po.act_array(act, x)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gxx_contraction_is_visible():
+    """Planted mistake: gelu with x + d*x^3 and exp's product each rounded
+    on their own (no contraction) differs from the restatement on many
+    inputs, so the bitwise check above can tell the two apart."""
+    x = I.uniform(11, 0, (1 << 16,), -6, 6)
+    y = po.act_array("gelu", x)
+    f = np.float32
+    x3 = x * (x * x)
+    inner = f(0.7978845608) * (x + f(0.044715) * x3)
+    two = (f(2.0) * inner).astype(np.float32)
+    two = np.minimum(np.maximum(two, f(-88.0)), f(88.0))
+    r = two * f(1.4426950408889634)
+    ri = np.floor(r)
+    rf = (r - ri).astype(np.float32)
+    p = np.full_like(rf, f(0.000154040))
+    for c in (0.001333356, 0.009614425, 0.055495506, 0.240226507, 0.693147180, 1.0):
+        p = (p.astype(np.float64) * rf + f(c)).astype(np.float32)  # fma: one rounding
+    e = (np.ldexp(np.float32(1.0), ri.astype(np.int32)).astype(np.float32) * p).astype(np.float32)
+    t = ((e - f(1.0)) / (e + f(1.0))).astype(np.float32)
+    twice_rounded = (f(0.5) * (x * (f(1.0) + t))).astype(np.float32)
+    assert np.count_nonzero(twice_rounded != y) > 100
+
+
+def test_fused_gelu_matches_gxx_build(gxx_probe):
+    """fusedGelu (FusedKernels.h:606-627): the vector groups and the tanhf
+    tail (where g++ fuses x + (0.044715*x*x)*x), bit for bit; both sides call
+    the same libm tanhf."""
+    for n in (5, 16, 37, 1000, 4099):
+        x = I.uniform(12, n, (n,), -6, 6)
+        want = np.empty_like(x)
+        gxx_probe.probe_fused_gelu(_fp(want), _fp(x), n)
+        np.testing.assert_array_equal(po.fused_gelu(x).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("act", ["none", "relu", "sigmoid", "tanh", "gelu"])
+def test_tiled_gemm_matches_gxx_build(gxx_probe, act):
+    """tiledMatmulWithActivation (FusedKernels.h:378-458) restated, against
+    the g++ build of the same loops, bit for bit: the fmadd chains reloaded
+    between K slices, the scalar columns past each tile's last 16-wide block
+    (an fma chain after g++'s contraction of `sum += a*b`) and both
+    epilogues, at ragged shapes and tiles with tails in every dimension."""
+    for (M, N, K, tiles) in ((37, 53, 71, (16, 32, 16)), (64, 48, 96, (32, 32, 128)),
+                             (8, 21, 7, (16, 16, 4)), (33, 100, 300, (16, 48, 64))):
+        A = I.uniform(13, M, (M, K), -1, 1)
+        B = I.uniform(13, N, (K, N), -1, 1)
+        want = np.empty((M, N), np.float32)
+        gxx_probe.probe_tiled(_fp(A), _fp(B), _fp(want), M, N, K, *tiles, po.ACT[act])
+        got = po.tiled_matmul_act(A, B, act, tiles=tiles)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=str((M, N, K, tiles)))
+
+
 def test_activation_closed_forms():
     x = np.float32([0.0, 1.0, -1.0, 3.0])
     assert list(po.act_array("relu", np.float32([-1.0, -0.0, 2.0, np.nan]))) == [0.0, 0.0, 2.0, 0.0]
@@ -105,22 +215,16 @@ def test_activation_closed_forms():
     assert po.act_array("gelu", np.float32([0.0]))[0] == 0.0
     assert po.act_array("silu", np.float32([0.0]))[0] == 0.0
     np.testing.assert_array_equal(po.act_array("none", x), x)
-    # gelu = 0.5 x (1 + tanh(u)) reproduced from the restated tanh and IEEE float32 ops
-    xs = np.float32([0.5, -0.75, 2.25])
-    for v in xs:
-        inner = np.float32(0.7978845608) * (v + np.float32(0.044715) * (v * (v * v)))
-        t = po.act_array("tanh", np.float32([inner]))[0]
-        assert po.act_array("gelu", np.float32([v]))[0] == np.float32(0.5) * (v * (np.float32(1.0) + t))
 
 
 def test_fused_gelu_matches_vector_path_and_tail():
     x = I.uniform(1, 0, (37,), -4, 4)
     y = po.fused_gelu(x)
     np.testing.assert_array_equal(y[:32], po.act_array("gelu", x[:32]))
-    # the last 5 elements take the tanhf tail (FusedKernels.h:614-617)
-    t = x[32:].astype(np.float32)
-    tail = np.float32(0.5) * t * (np.float32(1.0) + np.tanh(
-        np.float32(0.7978845608) * (t + np.float32(0.044715) * t * t * t)))
+    # the last 5 elements take the tanhf tail (FusedKernels.h:614-617): within
+    # fp32 rounding of the fp64 formula
+    t = x[32:].astype(np.float64)
+    tail = 0.5 * t * (1.0 + np.tanh(0.7978845608 * (t + 0.044715 * t ** 3)))
     np.testing.assert_allclose(y[32:], tail, rtol=2e-6, atol=1e-7)
 
 

@@ -5,7 +5,12 @@ jules_hip_w8a16_gemm_bias_act with a caller workspace (same kernels, fixed
 reduction order) on consecutive calls whose sizes shrink, so the second call
 runs on the scratch the first one left behind; the largest shape that fits the
 static scratch works, and one column tile more is rejected before any launch;
-captured once in a HIP graph, the call replays correctly with new inputs."""
+captured once in a HIP graph, the call replays correctly with new inputs;
+after every pattern of calls (different split counts back to back, graph
+replays) the per-tile arrival counters in the static array are back at 0."""
+import ctypes
+
+import numpy as np
 import pytest
 import torch
 
@@ -48,6 +53,36 @@ def test_noalloc_equals_workspace_entry_point(dev, act, with_bias):
         assert st == OK, _lib.lib().jules_hip_last_error()
         torch.cuda.synchronize()
         assert torch.equal(y, ref)
+
+
+def _counters():
+    out = (ctypes.c_uint32 * 1024)()
+    st = _lib.lib().jules_hip_w8a16_noalloc_counters(ctypes.cast(out, ctypes.c_void_p), 1024)
+    assert st == OK, _lib.lib().jules_hip_last_error()
+    return np.frombuffer(out, dtype=np.uint32).copy()
+
+
+def test_noalloc_counters_return_to_zero(dev):
+    """Calls whose split-K plans differ (K = 64, 1024, 8192, 2056: from one
+    split to eight) back to back on one stream, with no synchronisation in
+    between: every call's results equal the workspace entry point's, and the
+    counter words of all 1024 column tiles read 0 afterwards (each tile's
+    last arrival wraps its counter back to 0 in the same atomic)."""
+    assert not _counters().any()
+    shapes = ((8, 8192, 8192, 20), (4, 3072, 64, 21), (8, 8192, 1024, 22), (1, 16384, 2056, 23),
+              (8, 8192, 8192, 24))
+    outs, refs = [], []
+    for M, N, K, seed in shapes:
+        case(f"w8a16 noalloc counters {M}x{N}x{K}")
+        x, W, scale, bias = _operands(dev, M, N, K, seed)
+        y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        assert _noalloc(x, W, scale, bias, "silu", y) == OK, _lib.lib().jules_hip_last_error()
+        outs.append(y)
+        refs.append(ops.w8a16_gemm(x, W, scale, bias, "silu"))
+    torch.cuda.synchronize()
+    for (M, N, K, _), y, ref in zip(shapes, outs, refs):
+        assert torch.equal(y, ref), (M, N, K)
+    assert not _counters().any()
 
 
 def test_noalloc_size_limit(dev):
@@ -96,3 +131,4 @@ def test_noalloc_graph_replay(dev):
         ref = ops.w8a16_gemm(x, W, scale, bias, "silu")
         torch.cuda.synchronize()
         assert torch.equal(y, ref), f"replay {i}"
+    assert not _counters().any()
