@@ -53,7 +53,10 @@ def test_f32_descriptor_bit_exact(dev, name, act, with_bias, M, N, K):
     A, B, bias = I.gemm_inputs(M, N, K, "f32", seed=M + K)
     y = to_np(_call(dev, name, with_bias, A, B, bias, torch.float32))
     np.testing.assert_array_equal(y, po.matmul_bias_act(A, B, bias if with_bias else None, act))
-    tol = 1.5e-5 if act == "tanh" else I.TOL["f32"]  # the reference's own fast_tanh error
+    # the reference's fast_tanh, (e^2x - 1)/(e^2x + 1) on its degree-6
+    # fast_exp (1.74e-5 relative), is itself up to ~1.5e-5 from fp64 on these
+    # inputs; bit-exact parity inherits that, so tanh is held to 2e-5
+    tol = 2e-5 if act == "tanh" else I.TOL["f32"]
     assert I.rel_err(y, po.gemm64(A, B, bias if with_bias else None, act)) < tol
 
 
