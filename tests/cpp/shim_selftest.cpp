@@ -243,6 +243,48 @@ int main(int argc, char** argv) {
         (void)hipFree(dc);
     }
 
+    // blasMatmul on a skinny product (one 64 x 64 output tile, K = 4096): the
+    // library splits K across workgroups and applies alpha, beta (reading C)
+    // and the transposes in its split-K reduction.  Checked here against an
+    // fp64 product of the same inputs, normwise within 1e-5.
+    {
+        constexpr int SM = 64, SN = 64, SK = 4096;
+        uint32_t seed = 12345u;
+        auto uni = [&]() {  // uniform [-1, 1)
+            seed = seed * 1664525u + 1013904223u;
+            return (float)((seed >> 8) * (1.0 / 16777216.0) * 2.0 - 1.0);
+        };
+        std::vector<float> sa((size_t)SM * SK), sb((size_t)SK * SN), sc0((size_t)SM * SN);
+        for (float& v : sa) v = uni();
+        for (float& v : sb) v = uni();
+        for (float& v : sc0) v = uni();
+        for (int ta = 0; ta < 2; ++ta)
+            for (int tb = 0; tb < 2; ++tb) {
+                const std::string n = "blas_skinny_t" + std::to_string(ta) + std::to_string(tb);
+                step(n.c_str());
+                std::vector<float> sc = sc0;
+                const float alpha = 0.75f, beta_ = -1.25f;
+                blasMatmul(sa.data(), sb.data(), sc.data(), SM, SN, SK, alpha, beta_, ta, tb);
+                ok_status(n.c_str());
+                double num = 0.0, den = 0.0;
+                for (int i = 0; i < SM; ++i)
+                    for (int j = 0; j < SN; ++j) {
+                        double acc = 0.0;
+                        for (int k = 0; k < SK; ++k) {
+                            // op(A)[i,k], op(B)[k,j] with the reference's storage:
+                            // A [M,K] or [K,M], B [K,N] or [N,K]
+                            const double a = ta ? sa[(size_t)k * SM + i] : sa[(size_t)i * SK + k];
+                            const double b = tb ? sb[(size_t)j * SK + k] : sb[(size_t)k * SN + j];
+                            acc += a * b;
+                        }
+                        const double ref = alpha * acc + beta_ * (double)sc0[(size_t)i * SN + j];
+                        num = std::fmax(num, std::fabs(ref - sc[(size_t)i * SN + j]));
+                        den = std::fmax(den, std::fabs(ref));
+                    }
+                CHECK(num / den < 1e-5);
+            }
+    }
+
     // ---- fusedGelu: host, device, in place on both --------------------------
     step("fusedGelu");
     std::vector<float> g(GELU_N);
