@@ -29,12 +29,14 @@ def test_mfma_ceiling_runs(dev, workgroups, iters):
     assert np.array_equal(a, out.cpu().numpy())
 
 
-def test_hbm_read_floor_reads_every_chunk_once(dev):
+@pytest.mark.parametrize("n", [(1 << 20) + 16 * 37, (9 << 20) + 16 * 37, (20 << 20) + 16 * 5])
+def test_hbm_read_floor_reads_every_chunk_once(dev, n):
     """XOR over all lanes' results equals the XOR of every 4-byte word of the
-    buffer: each 16-byte chunk is read exactly once (grid-stride tail
-    included)."""
-    case("hbm read floor: every chunk read once")
-    n = (1 << 20) + 16 * 37  # not a multiple of the grid's stride
+    buffer: each 16-byte chunk is read exactly once.  256 workgroups x 256
+    lanes read 1 MiB per round; the sizes give 1, 9 and 20 whole rounds (the
+    8-deep load ring not used, used without its steady-state loop, and with
+    it) plus a partial last round."""
+    case(f"hbm read floor: every chunk read once, {n} bytes")
     host = np.random.default_rng(3).integers(-2**31, 2**31 - 1, n // 4, dtype=np.int64).astype(np.int32)
     buf = torch.from_numpy(host).to(dev)
     out = torch.empty(256 * 256, dtype=torch.int32, device=dev)
