@@ -47,23 +47,29 @@ constexpr float kNegInf = -__builtin_huge_valf();
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
 // Workgroup -> (head, query tile).  Workgroups are dealt to the 8 XCDs round
-// robin; the mapping gives each XCD whole heads (head = 8*j + xcd), taken in
-// pairs: the query tiles of heads j = 2g and 2g+1 are interleaved, heaviest
-// (causal: most keys) first.  The workgroups an XCD runs at once then span
-// about two heads, whose K and V (2 MiB each at S=4096, D=128) stay in that
-// XCD's 4 MiB L2 instead of being re-read from HBM by every query tile, and
-// consecutive workgroups shrink in size across the pair, so the CUs that
-// finish early take the next heavy ones (one head at a time, heaviest first,
-// left a ~5 % tail of CUs idle behind the last heads' heavy tiles).
+// robin; the mapping gives each XCD whole heads (head = 8*j + xcd), taken four
+// at a time: the query tiles of heads j = 4g .. 4g+3 are interleaved, heaviest
+// (causal: most keys) first.  The workgroups an XCD runs at once then span a
+// few heads whose K and V tiles are read by neighbouring query tiles close
+// together in time, so they come from that XCD's L2 rather than HBM, and the
+// CUs that finish early take the next heavy tiles.
+// Why four: inside an XCD workgroups start in order and are dealt to its 4
+// shader engines in a fixed rotation (timestamps with HW_ID show it); a
+// workgroup waits for a free CU on its own engine even when others are idle.
+// With four heads interleaved the four engines receive identical sequences of
+// tile sizes.  Two heads interleaved gave two engines all the even query
+// tiles and two all the odd ones, one key tile per workgroup apart: the
+// lighter engines idled behind the in-order dispatch (30.3 of 32 CUs busy on
+// average at C4's shape, causal; 1.103 -> 1.082 ms with four).
 __device__ __forceinline__ void block_coords(int BH, int nq, int bq, int* bh, int* q0) {
     const int b = blockIdx.x;
     int head, qi;
     if ((BH & 7) == 0) {
         const int xcd = b & 7, i = b >> 3;
         const int J = BH >> 3;                   // heads of this XCD
-        const int g = i / (2 * nq), r = i - g * 2 * nq;
-        const int gs = min(2, J - 2 * g);        // heads in this pair (1 for an odd last one)
-        head = 8 * (2 * g + r % gs) + xcd;
+        const int g = i / (4 * nq), r = i - g * 4 * nq;
+        const int gs = min(4, J - 4 * g);        // heads in this group (fewer in a last one)
+        head = 8 * (4 * g + r % gs) + xcd;
         qi = r / gs;
     } else {
         head = b / nq;
