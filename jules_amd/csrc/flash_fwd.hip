@@ -544,19 +544,32 @@ __device__ __forceinline__ void flash_bf16_body(
     // ---- epilogue: O = acc / l, bf16; lse = (m + log2 l) * ln 2 ----
     const float l_tot = pair_sum(l_run);
     const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-    if (qrow < S) {
-        uint16_t* Orow = O + hoff + (int64_t)qrow * D;
+    // The rows go out through LDS, which every wave has finished with at the
+    // last barrier: each wave writes its 32 rows of O to its own 32 x D
+    // region (16-byte unit u of row r at u ^ (r % U), so the 32 rows a write
+    // serves spread over the banks), then reads them back a row-contiguous
+    // 16 bytes per lane, so one store instruction writes 64 / U whole rows
+    // instead of 16 bytes of each of 32 rows.
+    constexpr int U = D / 8;                    // 16-byte units per row
+    constexpr int RPI = 64 / U;                 // rows per store instruction
+    uint8_t* stg = sm + wave * 32 * D * 2;
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt)
+    for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-                u32x2_t w;
-                w[0] = pack_bf16x2(acc_o[dt][4 * jb + 0] * inv, acc_o[dt][4 * jb + 1] * inv);
-                w[1] = pack_bf16x2(acc_o[dt][4 * jb + 2] * inv, acc_o[dt][4 * jb + 3] * inv);
-                *reinterpret_cast<u32x2_t*>(Orow + dt * 32 + 8 * jb + 4 * g) = w;
-            }
-        if (lse && g == 0)
-            lse[(int64_t)bh * S + qrow] = (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f;
+        for (int jb = 0; jb < 4; ++jb) {
+            u32x2_t w;
+            w[0] = pack_bf16x2(acc_o[dt][4 * jb + 0] * inv, acc_o[dt][4 * jb + 1] * inv);
+            w[1] = pack_bf16x2(acc_o[dt][4 * jb + 2] * inv, acc_o[dt][4 * jb + 3] * inv);
+            const int u = 4 * dt + jb;          // columns 8u .. 8u+7 of the row; lane g holds half g
+            *reinterpret_cast<u32x2_t*>(stg + col * (D * 2) + ((u ^ (col & (U - 1))) << 4) + 8 * g) = w;
+        }
+    if (lse && g == 0 && qrow < S)
+        lse[(int64_t)bh * S + qrow] = (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f;
+#pragma unroll
+    for (int s = 0; s < U / 2; ++s) {
+        const int r = s * RPI + lane / U, u = lane % U;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stg + r * (D * 2) + ((u ^ (r & (U - 1))) << 4));
+        if (qw0 + r < S) *reinterpret_cast<u32x4_t*>(O + hoff + (int64_t)(qw0 + r) * D + 8 * u) = v;
     }
 }
 
