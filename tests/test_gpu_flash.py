@@ -98,10 +98,12 @@ def test_c4_full_size_bf16(dev):
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("B,H,S,D", [(3, 8, 300, 128), (1, 24, 257, 64)])
+@pytest.mark.parametrize("B,H,S,D", [(3, 8, 300, 128), (1, 24, 257, 64), (5, 8, 300, 128),
+                                     (3, 16, 130, 128), (1, 56, 257, 64)])
 def test_odd_heads_per_xcd_against_fp64(dev, dt, causal, B, H, S, D):
-    """B*H = 24: three heads per XCD in the head-pair workgroup order (one
-    pair incomplete)."""
+    """B*H = 24, 40, 48, 56: 3, 5, 6 and 7 heads per XCD, so the workgroup
+    order's groups of four interleaved heads end with an incomplete group of
+    3, 1, 2 and 3 heads."""
     case(f"flash {dt} odd J causal={causal} [{B},{H},{S},{D}]")
     Q, K, V = I.attn_inputs(B, H, S, D, dt, seed=B * H + S)
     y = to_np(_run(dev, Q, K, V, dt, causal))
