@@ -151,8 +151,10 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rows_kernel(
     // Groups of KU k-steps.  The B row segments of group g+PB are loaded while
     // group g is computed (a ring of PB groups in registers).  Prefetches past
     // the last group reload the last group (never used), so every load is
-    // unconditional.
-    constexpr int PB = 8;
+    // unconditional.  One row per wave (the grids with few waves) keeps 12
+    // groups in flight (48 loads; g1-g3 5-9 % faster than 8), two rows 8
+    // (12 made C1 3 % slower).
+    constexpr int PB = RW == 1 ? 12 : 8;
     const int ng = K / KU;
     const int64_t nstride = N;
     float bq[PB][KU];
