@@ -53,10 +53,12 @@ constexpr int BOWN = BW * 32;    // keys (dK/dV pass) or queries (dQ pass) a wor
 constexpr int BSTEP = 64;        // query (dK/dV) or key (dQ) rows per loop step
 
 // Workgroup -> (head, block rank), rank 0 the block with the longest causal
-// range.  The forward's order: workgroups are dealt to the 8 XCDs round robin,
-// each XCD takes whole heads (head = 8*j + xcd) two at a time with their
-// blocks interleaved, longest first, so the heads' operands stay in that XCD's
-// L2 and the CUs that finish early take the next long blocks.
+// range.  Workgroups are dealt to the 8 XCDs round robin; each XCD takes whole
+// heads (head = 8*j + xcd) two at a time with their blocks interleaved,
+// longest first, so the heads' operands stay in that XCD's L2 and the CUs
+// that finish early take the next long blocks.  (The forward interleaves four
+// heads, which gives the XCD's four shader engines equal work there; with two
+// workgroups per CU here, four heads measured the same as two.)
 __device__ __forceinline__ void bwd_block(int nblk, int* bh, int* rank) {
     const int b = blockIdx.x, BH = gridDim.x / nblk;
     if ((BH & 7) == 0) {
