@@ -27,7 +27,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", f"-I{INCLUDE}", f"-
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-munsafe-fp-atomics"]
 
-SOURCES = ["gemm_f32.hip", "gemm_bf16.hip", "flash_fwd.hip", "flash_bwd.hip", "flash_pad.hip", "w8a16.hip", "w8a16_packed.hip", "matmul_int8.hip",
+SOURCES = ["gemm_f32.hip", "gemm_bf16.hip", "flash_fwd.hip", "flash_bwd.hip", "flash_bwd_dq.hip", "flash_pad.hip", "w8a16.hip", "w8a16_packed.hip", "matmul_int8.hip",
            "rowops.hip", "mlp.hip", "calib.hip", "pjrt_ops.hip", "scratch.hip", "capi.cpp", "kernel_shims.cpp",
            "pjrt.cpp"]
 

@@ -16,8 +16,9 @@
 //   1. dvec = rowsum(dO * O) in fp32 (HBM-bound);
 //   2. dK, dV: a workgroup owns 128 keys (4 waves x 32) and walks the query
 //      blocks of 64 (from the diagonal on, if causal);
-//   3. dQ: a workgroup owns 128 queries (4 waves x 32) and walks the key
-//      blocks of 64 (up to the diagonal, if causal).
+//   3. dQ (flash_bwd_dq.hip): a workgroup owns 256 queries (8 waves x 32)
+//      and walks the key units of 32 (up to the diagonal, if causal) in the
+//      forward kernel's ping-pong.
 // The dQ pass recomputes P and dP instead of accumulating dQ across key
 // blocks with atomics.
 //
@@ -43,14 +44,11 @@
 namespace jh {
 namespace {
 
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int BW = 4;            // waves per workgroup
 constexpr int BT = BW * 64;      // threads per workgroup
 constexpr int BOWN = BW * 32;    // keys (dK/dV pass) or queries (dQ pass) a workgroup owns
-constexpr int BSTEP = 64;        // query (dK/dV) or key (dQ) rows per loop step
 
 // Workgroup -> (head, block rank), rank 0 the block with the longest causal
 // range.  Workgroups are dealt to the 8 XCDs round robin; each XCD takes whole
@@ -113,21 +111,6 @@ template <int D>
 __device__ __forceinline__ bf16x8_t row_frag(const uint8_t* tile, int row, int ks, int g) {
     return as_bf16x8(*reinterpret_cast<const u32x4_t*>(tile + row * BwdCfg<D>::PITCH +
                                                        (16 * ks + 8 * g) * 2));
-}
-
-// Transposed fragment: column (32 dt + lane%32) of the 8 rows
-// {rb + 4g + 0..3, rb + 8 + 4g + 0..3} of a [rows][D] tile.
-template <int D>
-__device__ __forceinline__ bf16x8_t tr_frag(const uint8_t* tile, int rb, int dt, int lane) {
-    const int g = lane >> 5, vs = lane & 15, vdh = (lane >> 4) & 1;
-    const int r = rb + 4 * g + (vs >> 2);
-    const int chunk = 8 * dt + 4 * vdh + (vs & 3);  // 8-byte chunk of the row
-    const uint8_t* p = tile + r * BwdCfg<D>::PITCH + chunk * 8;
-    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * BwdCfg<D>::PITCH));
-    typedef short i16x8_t __attribute__((ext_vector_type(8)));
-    const i16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return __builtin_bit_cast(bf16x8_t, v);
 }
 
 template <int I, int N, typename F>
@@ -194,51 +177,6 @@ __device__ __forceinline__ void tr_pipeline(uint32_t base, O&& off, U&& use) {
         constexpr int later = (m + L < NM ? L : NM - 1 - m);  // MFMAs whose reads follow m's
         use(mi, tr_wait<2 * later>(ring[m % R]));
     });
-}
-
-// Row fragments (16-byte reads) in the same way: MFMA m takes RPM reads,
-// read j at base + off(m, j) (a compile-time offset), use(m, frags) issues it.
-template <int OFF>
-__device__ __forceinline__ u32x4_t b128_issue(uint32_t addr) {
-    static_assert(OFF >= 0 && OFF < 65536, "16-bit LDS offset");
-    u32x4_t v;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
-    return v;
-}
-template <int N>
-__device__ __forceinline__ void b128_wait(u32x4_t& a) {
-    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(N) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void b128_wait(u32x4_t& a, u32x4_t& b) {
-    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
-}
-template <int NM, int RPM, int L, typename O, typename U>
-__device__ __forceinline__ void row_pipeline(uint32_t base, O&& off, U&& use) {
-    static_assert(RPM == 1 || RPM == 2, "one or two reads per MFMA");
-    constexpr int R = L + 2;
-    u32x4_t ring[R][RPM];
-    auto issue = [&](auto mi) {
-        constexpr int m = decltype(mi)::value;
-        static_for<0, RPM>([&](auto ji) {
-            constexpr int j = decltype(ji)::value;
-            ring[m % R][j] = b128_issue<decltype(off(ic<m>{}, ic<j>{}))::value>(base);
-        });
-    };
-    static_for<0, L>([&](auto mi) { issue(mi); });
-    static_for<0, NM>([&](auto mi) {
-        constexpr int m = decltype(mi)::value;
-        if constexpr (m + L < NM) issue(ic<m + L>{});
-        constexpr int later = (m + L < NM ? L : NM - 1 - m);
-        if constexpr (RPM == 1) b128_wait<later>(ring[m % R][0]);
-        else b128_wait<2 * later>(ring[m % R][0], ring[m % R][1]);
-        use(mi, ring[m % R]);
-    });
-}
-
-template <int D>
-__device__ __forceinline__ uint32_t row_addr(const uint8_t* tile, int row, int ks, int g) {
-    return (uint32_t)(uintptr_t)(tile + row * BwdCfg<D>::PITCH + (16 * ks + 8 * g) * 2);
 }
 
 __device__ __forceinline__ f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
@@ -457,160 +395,7 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
         }
 }
 
-// ---- 3. dQ ----------------------------------------------------------------------
-// 4 waves x 32 queries, two workgroups per CU: the two waves of a SIMD come
-// from different workgroups, whose barriers are independent, so one's MFMAs
-// overlap the other's exp and dS arithmetic (8-wave workgroups kept both in
-// step and measured 1-3 % slower).  K/V tiles of 64 keys are double buffered
-// in LDS: the global loads of tile t+1 are issued into registers before tile
-// t is multiplied and stored to the other buffer after, one barrier per tile.
-// Causal: a wave skips the tiles wholly above its last query.
-constexpr int QW = 4;             // waves per dQ workgroup
-constexpr int QT = QW * 64;
-constexpr int QOWN = QW * 32;     // queries per dQ workgroup
-
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(QT, 2) void flash_bwd_dq_kernel(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dvec,
-    uint16_t* __restrict__ dQ, int S, float scale) {
-    using C = BwdCfg<D>;
-    constexpr int UNITS = D / 8;                      // 16-byte units per row
-    constexpr int PF = 2 * BSTEP * UNITS / QT;        // prefetched units per thread (K then V)
-    __shared__ __attribute__((aligned(16))) uint8_t kv_t[2][2][BSTEP * C::PITCH];  // [buf][K, V]
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const int g = lane >> 5, col = lane & 31;
-    const int nqb = (S + QOWN - 1) / QOWN;
-    int bh, rank;
-    bwd_block(nqb, &bh, &rank);
-    const int q0 = (nqb - 1 - rank) * QOWN;  // longest causal range first
-    const int64_t hoff = (int64_t)bh * S * D;
-    const uint16_t* Kh = K + hoff;
-    const uint16_t* Vh = V + hoff;
-    const float c = scale * kLog2e;
-
-    // this lane's query (S^T / dP^T column) and its Q, dO fragments (B operands)
-    const int q = q0 + wave * 32 + col;
-    const int qr = min(q, S - 1);
-    bf16x8_t qf[C::KS], of[C::KS];
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-        qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(Q + hoff + (int64_t)qr * D + 16 * ks + 8 * g));
-        of[ks] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(dO + hoff + (int64_t)qr * D + 16 * ks + 8 * g));
-    }
-    const float lse2 = lse[(int64_t)bh * S + qr] * kLog2e;
-    const float dvq = dvec[(int64_t)bh * S + qr];
-
-    // tile loads: unit e = tid + QT p of the 2 x 64 rows (K rows, then V rows)
-    u32x4_t pf[PF];
-    auto gload = [&](int kb) {
-#pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            const int e = tid + QT * p;
-            const int r = (e / UNITS) % BSTEP, u = e % UNITS;
-            const int64_t gr = min(kb + r, S - 1);
-            const uint16_t* src = (e / UNITS < BSTEP ? Kh : Vh) + gr * D + 8 * u;
-            pf[p] = *reinterpret_cast<const u32x4_t*>(src);
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            const int e = tid + QT * p;
-            const int r = (e / UNITS) % BSTEP, u = e % UNITS;
-            *reinterpret_cast<u32x4_t*>(&kv_t[buf][e / UNITS / BSTEP][r * C::PITCH + 16 * u]) = pf[p];
-        }
-    };
-
-    f32x16_t dq[C::DT];
-#pragma unroll
-    for (int i = 0; i < C::DT; ++i) dq[i] = zero16();
-
-    const int kv_end = CAUSAL ? min(S, q0 + QOWN) : S;
-    const int nt = (kv_end + BSTEP - 1) / BSTEP;  // >= 1
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int t = 0; t < nt; ++t) {
-        const int buf = t & 1, kb = t * BSTEP;
-        if (t + 1 < nt) gload(kb + BSTEP);
-        const uint8_t* k_t = kv_t[buf][0];
-        const uint8_t* v_t = kv_t[buf][1];
-        // causal: a tile wholly above this wave's last query adds nothing
-        if (!CAUSAL || kb <= q0 + wave_u * 32 + 31) {
-        // every key of the tile is < S and (causal) before every query of the
-        // wave (queries past S only feed dQ rows that are never stored)
-        const bool unmasked = kb + BSTEP <= S && (!CAUSAL || kb + BSTEP - 1 <= q0 + wave_u * 32);
-        // S^T = K Q^T, dP^T = V dO^T: 64 keys x this wave's 32 queries
-        bf16x8_t sb[2][2];  // dS^T as B operands: [32-key half][16-key step]
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            f32x16_t s = zero16(), dp = zero16();
-            // S^T and dP^T MFMAs alternate: m = 2 ks + which
-            // MFMA m reads V (odd m) or K, k-step m >> 1: v_t = k_t + BSTEP rows
-            row_pipeline<2 * C::KS, 1, 2>(
-                row_addr<D>(k_t, h * 32 + col, 0, g),
-                [](auto mi, auto) {
-                    constexpr int m = decltype(mi)::value;
-                    return ic<((m & 1) ? BSTEP * C::PITCH : 0) + 32 * (m >> 1)>{};
-                },
-                [&](auto mi, u32x4_t* f) {
-                    constexpr int m = decltype(mi)::value;
-                    if constexpr (m & 1) dp = mfma(as_bf16x8(f[0]), of[m >> 1], dp);
-                    else s = mfma(as_bf16x8(f[0]), qf[m >> 1], s);
-                });
-            // register r: key kb + h*32 + 8(r/4) + 4g + r%4; unmasked, then
-            // the last tile and the diagonal zero the masked elements (see
-            // the dK/dV pass)
-            float ds[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -lse2));
-                ds[r] = pv * (dp[r] - dvq);
-            }
-            if (!unmasked) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int k = kb + h * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (!(k < S && q < S && (!CAUSAL || k <= q))) ds[r] = 0.0f * (dp[r] - dvq);
-                }
-            }
-#pragma unroll
-            for (int t2 = 0; t2 < 2; ++t2) sb[h][t2] = pack8(ds + 8 * t2);
-        }
-        // dQ^T += K^T dS^T: A = K read transposed in the matching key order
-        // MFMA m = (dt, h, t2); the reads of MFMAs m+1 and m+2 are in flight
-        tr_pipeline<D, 4 * C::DT, 2>(
-            tr_addr<D>(k_t, 0, 0, lane),
-            [](auto mi) {
-                constexpr int m = decltype(mi)::value;
-                return ic<16 * (m & 3) * C::PITCH + 64 * (m >> 2)>{};
-            },
-            [&](auto mi, bf16x8_t a) {
-                constexpr int m = decltype(mi)::value, dt = m >> 2, h = (m >> 1) & 1, t2 = m & 1;
-                dq[dt] = mfma(a, sb[h][t2], dq[dt]);
-            });
-        }
-        if (t + 1 < nt) sstore(buf ^ 1);
-        __syncthreads();
-    }
-
-    // dQ = scale * dS K; register r of block dt: head dim 32 dt + 8(r/4) +
-    // 4g + r%4 of this lane's query: 4 consecutive d per 8-byte store
-    if (q >= S) return;
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-            const int d = 32 * dt + 8 * r4 + 4 * g;
-            u32x2_t o;
-            o[0] = pack_bf16x2(dq[dt][4 * r4] * scale, dq[dt][4 * r4 + 1] * scale);
-            o[1] = pack_bf16x2(dq[dt][4 * r4 + 2] * scale, dq[dt][4 * r4 + 3] * scale);
-            *reinterpret_cast<u32x2_t*>(dQ + hoff + (int64_t)q * D + d) = o;
-        }
-}
+// ---- 3. dQ: flash_bwd_dq.hip (an 8-wave ping-pong like the forward kernel) ----
 
 template <int D, bool CAUSAL>
 hipError_t launch_bwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, const uint16_t* O,
@@ -623,10 +408,9 @@ hipError_t launch_bwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, c
     const int nb = (S + BOWN - 1) / BOWN;
     hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, CAUSAL>), dim3(BH * nb), dim3(BT), 0, s, Q, K, V, dO,
                        lse, dvec, dK, dV, S, scale);
-    const int nqb = (S + QOWN - 1) / QOWN;
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, CAUSAL>), dim3(BH * nqb), dim3(QT), 0, s, Q, K, V, dO,
-                       lse, dvec, dQ, S, scale);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_flash_bwd_dq(D, CAUSAL, Q, K, V, dO, lse, dvec, dQ, BH, S, scale, s);
 }
 
 }  // namespace

@@ -53,6 +53,11 @@ size_t w8a16_partials_size(int M, int N, int K);
 hipError_t launch_w8a16_counters(int act, const uint16_t* x, const int8_t* W, const float* scale,
                                  const float* bias, uint16_t* y, int M, int N, int K,
                                  float* partials, uint32_t* counters, hipStream_t s);
+// dQ pass of the flash backward (flash_bwd_dq.hip); dvec = rowsum(dO * O)
+hipError_t launch_flash_bwd_dq(int D, bool causal, const uint16_t* Q, const uint16_t* K,
+                               const uint16_t* V, const uint16_t* dO, const float* lse,
+                               const float* dvec, uint16_t* dQ, int BH, int S, float scale,
+                               hipStream_t s);
 // W8A16 on the packed weight layout (w8a16_packed.hip): Wp holds
 // w8a16_packed_bytes(K, N) bytes, written by launch_w8a16_pack from
 // row-major W [K,N]
