@@ -16,6 +16,8 @@
 // computed, so their latency is paid once per launch, not once per slice.
 // The K tail is handled by a uniform trip count, never by zero padding (an
 // extra fma(0, b, acc) could turn a -0 partial sum into +0).
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 #include "tiles.hpp"
@@ -207,6 +209,190 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rows_kernel(
     }
 }
 
+
+// ---- row kernel with B streamed through an LDS ring by LDS DMA ----
+// Same work split and fma chains as gemm_f32_rows_kernel (a wave owns RW rows
+// x 64 columns, lane = column, A rows staged in LDS once), but the B column
+// block reaches LDS by LDS DMA through a ring of RD_NST stages of RD_KG k-rows,
+// so the bytes in flight are not bounded by the wave's registers, and the
+// workgroup's four waves share each B row instead of each loading it.  The
+// LDS reads (A as a broadcast b128 per row, B as 4 b32 per group of 4 k) run
+// RD_PD groups ahead; they are inline asm with explicit waits (through
+// builtins the compiler drains every DMA in flight before any LDS read).
+// Used when N % 4 == 0 and B is 16-byte aligned (16-byte DMA pieces).
+// At C1 (512^3): 16.0 us against 18.6 us for the register ring; g1 12.8 vs
+// 17.0, g3 9.0 vs 11.9 (32-row stages with 6 stages: 17.6 / 14.8 / 10.2).
+constexpr int RD_KG = 64;   // k rows per ring stage (16 KiB of B)
+constexpr int RD_NST = 4;   // ring stages
+constexpr int RD_PD = 3;    // groups of 4 k whose LDS reads are in flight
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_f(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for_f<I + 1, N>(f);
+    }
+}
+typedef __attribute__((address_space(3))) void lds_void_f;
+
+template <int OFF>
+__device__ __forceinline__ float rd_f32(uint32_t a) {
+    float v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ f32x4_t rd_f128(uint32_t a) {
+    f32x4_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
+    return v;
+}
+
+// Waits until at most N LDS reads are outstanding; the group's operands pass
+// through the asm, so no fma that uses them is scheduled above the wait.
+template <int N, int RW>
+__device__ __forceinline__ void rd_wait(f32x4_t (&a)[RW], float (&b)[4]) {
+    if constexpr (RW == 1)
+        asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(a[0]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]) : "n"(N) : "memory");
+    else
+        asm volatile("s_waitcnt lgkmcnt(%6)"
+                     : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])
+                     : "n"(N)
+                     : "memory");
+}
+
+template <int ACT, int RW>
+__global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ bias,
+    float* __restrict__ C, int M, int N, int K) {
+    extern __shared__ __attribute__((aligned(16))) float sdyn[];  // ring [RD_NST][RD_KG][64], then A [RW*RWV][Kp]
+    float* sB = sdyn;
+    float* sA = sdyn + RD_NST * RD_KG * 64;
+    const int Kp = (K + 3) & ~3;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * 64;
+    const int n = n0 + lane;
+    const int mb = blockIdx.y * RW * RWV;
+    const int nst = (K + RD_KG - 1) / RD_KG;
+
+    // stage rows mb .. mb + RW*RWV - 1 of A (rows past M repeat row M-1)
+    for (int i = threadIdx.x; i < RW * RWV * K; i += 64 * RWV) {
+        const int r = i / K, k = i - r * K;
+        sA[r * Kp + k] = A[(int64_t)min(mb + r, M - 1) * K + k];
+    }
+    __syncthreads();
+
+    // stage s of B: rows [32 s, 32 s + 32) x columns [n0, n0 + 64), 8 pieces
+    // of 4 rows (1 KiB); wave w moves pieces 2w and 2w+1.  Lane l of piece i
+    // moves row 4i + l/16, columns n0 + 4(l%16) .. +3.  The buffer covers the
+    // stage's rows that exist (none past the last stage: no traffic), so every
+    // call issues two instructions and the wait counts are constants.  Columns
+    // past N read the next row (or 0 past the end): they only feed outputs
+    // that are not stored.
+    auto copy_stage = [&](int s) {
+        const bool live = s < nst;
+        const int rows = live ? min(RD_KG, K - RD_KG * s) : 0;
+        const __amdgpu_buffer_rsrc_t src = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(B) + (int64_t)RD_KG * (live ? s : 0) * N, 0, (uint32_t)rows * (uint32_t)N * 4u,
+            0x00020000);
+#pragma unroll
+        for (int p = 0; p < RD_KG / 16; ++p) {
+            const int i = (RD_KG / 16) * wave + p;
+            const uint32_t vo = ((uint32_t)(4 * i + (lane >> 4)) * (uint32_t)N + (uint32_t)(n0 + 4 * (lane & 15))) * 4u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                src, (lds_void_f*)(sB + ((s % RD_NST) * RD_KG + 4 * i) * 64), 16, vo, 0, 0, 0);
+        }
+    };
+
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+    const uint32_t a0 = (uint32_t)(uintptr_t)(sA + wave * RW * Kp);
+    const uint32_t b0 = (uint32_t)(uintptr_t)(sB + lane);
+
+#pragma unroll
+    for (int p = 0; p < RD_NST - 1; ++p) copy_stage(p);
+    for (int s = 0; s < nst; ++s) {
+        // this wave's pieces of stage s have landed once the 2 (RD_NST - 2)
+        // instructions of the later stages are all that remain; the barrier
+        // makes every wave's pieces visible and ends every wave's reads of
+        // stage s - 1, whose slot the next copy reuses
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((RD_KG / 16) * (RD_NST - 2)) : "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        copy_stage(s + RD_NST - 1);
+        const int kv = min(RD_KG, K - RD_KG * s);   // k rows of this stage
+        const int k0 = RD_KG * s;
+        const uint32_t bs = b0 + (uint32_t)((s % RD_NST) * RD_KG * 64 * 4);
+        const int ng = kv >> 2;
+        // groups of 4 k: A as one b128 per row, B as 4 b32; a ring of RD_PD
+        // groups of reads in flight
+        f32x4_t a[RD_PD][RW];
+        float b[RD_PD][4];
+        auto rd = [&](int g, int slot) {
+#pragma unroll
+            for (int r = 0; r < RW; ++r) a[slot][r] = rd_f128<0>(a0 + (uint32_t)((r * Kp + k0 + 4 * g) * 4));
+            const uint32_t bg = bs + (uint32_t)(4 * g * 64 * 4);
+            b[slot][0] = rd_f32<0>(bg);
+            b[slot][1] = rd_f32<256>(bg);
+            b[slot][2] = rd_f32<512>(bg);
+            b[slot][3] = rd_f32<768>(bg);
+        };
+        if (ng == RD_KG / 4) {
+            // a full stage: fully unrolled, compile-time ring slots and waits
+            constexpr int NG = RD_KG / 4;
+            static_for_f<0, RD_PD>([&](auto ic) { rd(decltype(ic)::value, decltype(ic)::value); });
+            static_for_f<0, NG>([&](auto ic) {
+                constexpr int g = decltype(ic)::value, slot = g % RD_PD;
+                constexpr int later = (g + RD_PD - 1 < NG ? RD_PD - 1 : NG - 1 - g);  // groups read after g
+                rd_wait<later * (RW + 4), RW>(a[slot], b[slot]);
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    acc[r] = __builtin_fmaf(a[slot][r].x, b[slot][0], acc[r]);
+                    acc[r] = __builtin_fmaf(a[slot][r].y, b[slot][1], acc[r]);
+                    acc[r] = __builtin_fmaf(a[slot][r].z, b[slot][2], acc[r]);
+                    acc[r] = __builtin_fmaf(a[slot][r].w, b[slot][3], acc[r]);
+                }
+                if constexpr (g + RD_PD < NG) rd(g + RD_PD, slot);
+            });
+        } else {
+            // the last, partial stage: one group at a time
+            for (int g = 0; g < ng; ++g) {
+                rd(g, 0);
+                rd_wait<0, RW>(a[0], b[0]);
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    acc[r] = __builtin_fmaf(a[0][r].x, b[0][0], acc[r]);
+                    acc[r] = __builtin_fmaf(a[0][r].y, b[0][1], acc[r]);
+                    acc[r] = __builtin_fmaf(a[0][r].z, b[0][2], acc[r]);
+                    acc[r] = __builtin_fmaf(a[0][r].w, b[0][3], acc[r]);
+                }
+            }
+        }
+        // the k rows past the last full group (K % 4 in the last stage)
+        for (int k = 4 * ng; k < kv; ++k) {
+            float bk = rd_f32<0>(bs + (uint32_t)(k * 64 * 4));
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                float ak = rd_f32<0>(a0 + (uint32_t)((r * Kp + k0 + k) * 4));
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ak), "+v"(bk)::"memory");
+                acc[r] = __builtin_fmaf(ak, bk, acc[r]);
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the last stage (no traffic)
+    if (n >= N) return;
+    const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int m = mb + wave * RW + r;
+        if (m >= M) continue;
+        float v = acc[r];
+        if (bias) v = v + bv;
+        C[(int64_t)m * N + n] = activate<ACT>(v);
+    }
+}
+
 template <int BM, int BN, int BK, int TM, int TN, int ACT>
 hipError_t run(const float* A, const float* B, const float* bias, float* C, int M, int N, int K,
                hipStream_t s) {
@@ -250,6 +436,21 @@ hipError_t launch_gemm_f32_variant(int variant, int act, const float* A, const f
         hipLaunchKernelGGL(kern, grid, dim3(64 * RWV), lds, s, A, B, bias, C, M, N, K);
         return hipGetLastError();
     };
+    const bool dma = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(B) % 16) == 0;
+    auto rowsdma = [&](auto kern, int rw) {
+        dim3 grid((N + 63) / 64, (M + rw * RWV - 1) / (rw * RWV));
+        const size_t lds = ((size_t)RD_NST * RD_KG * 64 + (size_t)rw * RWV * ((K + 3) & ~3)) * sizeof(float);
+        hipLaunchKernelGGL(kern, grid, dim3(64 * RWV), lds, s, A, B, bias, C, M, N, K);
+        return hipGetLastError();
+    };
+    if (dma && variant == GV_F32_ROWS1) {
+        JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 1>, 1));
+        return e;
+    }
+    if (dma && variant == GV_F32_ROWS2) {
+        JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 2>, 2));
+        return e;
+    }
     switch (variant) {
     case GV_F32_ROWS1: JH_DISPATCH_ACT(act, ACT, e = rows(gemm_f32_rows_kernel<ACT, 1>, 1)); break;
     case GV_F32_ROWS2: JH_DISPATCH_ACT(act, ACT, e = rows(gemm_f32_rows_kernel<ACT, 2>, 2)); break;
