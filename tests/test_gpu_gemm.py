@@ -40,8 +40,9 @@ def test_f32_c1_bit_exact(dev, act):
 
 @pytest.mark.parametrize("M,N,K", [(1, 16, 1), (17, 32, 5), (65, 144, 257), (128, 96, 1000),
                                    (300, 640, 64), (2048, 2048, 96),
-                                   # row-wave kernel at its K limit (1 and 2 rows per wave: 32
-                                   # and 64 KiB of LDS), and one past it (LDS-tiled)
+                                   # row-wave kernel at its K limit (1 and 2 rows per wave, B
+                                   # through the LDS-DMA ring: 96 and 128 KiB of LDS), and one
+                                   # past it (LDS-tiled)
                                    (9, 144, 2048), (256, 512, 2048), (33, 64, 2100)])
 def test_f32_shapes_bit_exact(dev, M, N, K):
     case(f"gemm f32 {M}x{N}x{K}")
@@ -50,7 +51,11 @@ def test_f32_shapes_bit_exact(dev, M, N, K):
     np.testing.assert_array_equal(y, po.matmul_bias_act(A, B, bias, "gelu"))
 
 
-@pytest.mark.parametrize("M,N,K", [(5, 21, 7), (33, 50, 19)])
+@pytest.mark.parametrize("M,N,K", [(5, 21, 7), (33, 50, 19),
+                                   # N % 4 != 0: the row kernel with B in a register ring
+                                   # (the reference's published 64 x 10 x 256 shape); N % 4 == 0
+                                   # with a partial 64-column block: the LDS-DMA ring
+                                   (64, 10, 256), (40, 130, 300), (37, 132, 77)])
 def test_f32_ragged_n_against_fp64(dev, M, N, K):
     """N not a multiple of 16: the reference's tail columns use libm tanhf;
     the GPU keeps the vector-path activation, so parity is to the fp64 bar."""
