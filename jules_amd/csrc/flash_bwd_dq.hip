@@ -211,13 +211,16 @@ __global__ __launch_bounds__(512, 1) void flash_bwd_dq_pp_kernel(
 
     // ---- copy piece p of tile t: p < SEGW a K segment, else a V segment;
     // wave w moves segments w, w+8, ... of each operand tile.  Buffer loads
-    // over the head's rows: rows past S read 0 (their keys are masked) ----
+    // over the tile's rows that exist: rows past S read 0 (their keys are
+    // masked), and every offset stays small whatever S is ----
     const uint32_t sm0 = (uint32_t)(uintptr_t)sm;
-    const __amdgpu_buffer_rsrc_t ksrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(Kh), 0, (uint32_t)S * (uint32_t)C::ROW, 0x00020000);
-    const __amdgpu_buffer_rsrc_t vsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(Vh), 0, (uint32_t)S * (uint32_t)C::ROW, 0x00020000);
     auto dma_part = [&](int t, int p0, int p1) {
+        const int64_t tr0 = (int64_t)t * DQ_BKV;
+        const uint32_t bytes = (uint32_t)min(DQ_BKV, S - t * DQ_BKV) * (uint32_t)C::ROW;
+        const __amdgpu_buffer_rsrc_t ksrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(Kh + tr0 * D), 0, bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t vsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(Vh + tr0 * D), 0, bytes, 0x00020000);
 #pragma unroll
         for (int p = 0; p < PIECES; ++p) {
             if (p < p0 || p >= p1) continue;
@@ -225,8 +228,7 @@ __global__ __launch_bounds__(512, 1) void flash_bwd_dq_pp_kernel(
             const int seg = i * DQ_W + wave;
             const int r = seg * C::RPS + lane / C::UNITS;  // row within the tile
             const int up = lane % C::UNITS;                // physical 16-byte unit
-            // the whole offset in the range-checked register operand
-            const uint32_t vo = (uint32_t)((t * DQ_BKV + r) * C::ROW + ((up ^ dq_sw<D>(r)) << 4));
+            const uint32_t vo = (uint32_t)(r * C::ROW + ((up ^ dq_sw<D>(r)) << 4));
             uint8_t* dst = sm + (t % C::NSTAGE) * C::STAGE + seg * 1024;
             if (p < C::SEGW)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ksrc, (lds_void_dq*)dst, 16, vo, 0, 0, 0);
