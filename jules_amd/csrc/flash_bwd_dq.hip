@@ -10,21 +10,25 @@
 // unit of 32 keys (lane = query, 16 keys per lane), then dQ^T += K^T dS^T
 // with dS^T packed from the accumulator registers as the B operand and K^T
 // read from LDS with ds_read_b64_tr_b16.  The waves form two groups, A = waves
-// 0-3 and B = waves 4-7, one of each per SIMD, half a unit out of phase: in
-// each phase (closed by a barrier of all 8 waves) one group issues the MFMAs
-// of a unit (S^T_u, dP^T_u and the dQ^T product of unit u-1: 24 MFMAs at
-// D = 128) while the other turns its S^T, dP^T into dS^T on the vector ALU.
-//   group A: MFMA(u) in phase 2u,     VALU(u) in phase 2u+1;
-//   group B: MFMA(u) in phase 2u+1,   VALU(u) in phase 2u+2.
+// 0-3 and B = waves 4-7, one of each per SIMD, half a unit out of phase: one
+// group issues the MFMAs of a unit (S^T_u, dP^T_u and the dQ^T product of
+// unit u-1: 24 MFMAs at D = 128) while the other turns its S^T, dP^T into
+// dS^T on the vector ALU.  Step u is closed by one barrier of all 8 waves:
+//   group A: MFMA(u), then VALU(u);
+//   group B: VALU(u-1), then MFMA(u).
+// The groups meet only at the barrier, so a group whose first half ends
+// early goes on with its second instead of waiting for the other group (a
+// barrier between the halves measured 2-3% slower over the whole backward).
 // A lane's lse and dvec are per-query scalars, so there is no running
 // statistic to carry between units.
 //
 // K and V tiles of 64 keys (two units) go HBM -> LDS by LDS DMA through a ring
 // of 4 stages; tile t in stage t % 4.  The K half of tile t+2 is copied at
-// the start of phase 4t, its V half at the start of phase 4t+2, and tile t+1
+// the start of step 2t, its V half at the start of step 2t+1, and tile t+1
 // has landed (each wave waits for its own copies, then the barrier) at the
-// end of phase 4t+3, before its first use in phase 4t+4.  Tile t-2, which
-// stage (t+2) % 4 held, was last read in phase 4t-3.
+// end of step 2t+1, before its first use in step 2t+2.  Tile t-2, which
+// stage (t+2) % 4 held, was last read in step 2t-2 (MFMA(2t-2) reads K^T of
+// unit 2t-3 for its dQ^T product).
 // Both tiles are row-major [key][d], 16-byte unit u of row r at u ^ sw(r).
 // V is read by rows (ds_read_b128: 8 d of one key per lane, 16 rows per
 // clock); K by rows too and, for dQ, transposed (ds_read_b64_tr_b16: a
@@ -345,12 +349,12 @@ __global__ __launch_bounds__(512, 1) void flash_bwd_dq_pp_kernel(
     auto copy_v = [&](int t) {
         if (t < n_t) dma_part(t, C::SEGW, PIECES);
     };
-    // start of phase 2u: unit u = 2t copies tile t+2's K half, u = 2t+1 its V half
+    // start of step u: unit u = 2t copies tile t+2's K half, u = 2t+1 its V half
     auto copies = [&](int u) {
         if (u & 1) copy_v((u >> 1) + 2);
         else copy_k((u >> 1) + 2);
     };
-    // end of phase 2u+1 for odd u = 2t+1: tile t+1 has landed
+    // end of step u for odd u = 2t+1: tile t+1 has landed
     auto land = [&](int u) {
         if ((u & 1) && (u >> 1) + 1 < n_t) dq_vm((u >> 1) + 2 < n_t ? PIECES : 0);
     };
@@ -379,42 +383,43 @@ __global__ __launch_bounds__(512, 1) void flash_bwd_dq_pp_kernel(
 
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
+    // Step 0 is split in two (group B has no VALU work yet, and starting it
+    // half a unit late puts the groups out of phase); the last step is split
+    // the same way for the tail of group B.
     if (grp == 0) {
         copies(0);
         if (need(0)) mfma_phase(0, yes{}, no{});
-        dq_barrier();  // phase 0
+        dq_barrier();
         if (need(0)) valu_phase(0);
         land(0);
-        dq_barrier();  // phase 1
+        dq_barrier();  // step 0
         for (int u = 1; u < U; ++u) {
             copies(u);
             if (need(u - 1)) mfma_phase(u, yes{}, yes{});
-            dq_barrier();  // phase 2u
             if (need(u)) valu_phase(u);
             land(u);
-            dq_barrier();  // phase 2u+1
+            dq_barrier();  // step u
         }
         if (need(U - 1)) mfma_phase(U, no{}, yes{});
-        dq_barrier();  // phase 2U
-        dq_barrier();  // phase 2U+1
+        dq_barrier();
+        dq_barrier();  // step U
     } else {
         copies(0);
-        dq_barrier();  // phase 0
+        dq_barrier();
         if (need(0)) mfma_phase(0, yes{}, no{});
         land(0);
-        dq_barrier();  // phase 1
+        dq_barrier();  // step 0
         for (int u = 1; u < U; ++u) {
             copies(u);
             if (need(u - 1)) valu_phase(u - 1);
-            dq_barrier();  // phase 2u
             if (need(u - 1)) mfma_phase(u, yes{}, yes{});
             land(u);
-            dq_barrier();  // phase 2u+1
+            dq_barrier();  // step u
         }
         if (need(U - 1)) valu_phase(U - 1);
-        dq_barrier();  // phase 2U
+        dq_barrier();
         if (need(U - 1)) mfma_phase(U, no{}, yes{});
-        dq_barrier();  // phase 2U+1
+        dq_barrier();  // step U
     }
 
     // ---- epilogue: dQ = scale * acc, bf16, through LDS (free after the last
