@@ -102,6 +102,7 @@ __device__ __forceinline__ u32x2_t dq_tr16(uint32_t addr) {
 }
 template <int N>
 __device__ __forceinline__ void dq_lgkm(u32x4_t& v) {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt is a 4-bit count");
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N) : "memory");
 }
 __device__ __forceinline__ void dq_vm(int n) {
