@@ -676,8 +676,13 @@ def ops_scale(D):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # The warmup covers the power controller's transient: after an idle spell
+    # the first C4 launches run at a boosted clock, the next few are throttled
+    # well below the sustained rate (up to 1.36 ms against ~1.06-1.09 ms), and
+    # the clock settles over ~25 launches (kernel trace of this script).  30
+    # warmup steps put the 40 timed steps at the sustained rate.
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-calib", action="store_true", help="skip the MFMA ceiling calibration")
     ap.add_argument("--only", default="", help="comma list of per-config runs (default all)")
