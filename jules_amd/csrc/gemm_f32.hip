@@ -113,113 +113,26 @@ __global__ __launch_bounds__((BM / TM) * (BN / TN)) void gemm_f32_kernel(
 
 // Small problems (C1: 512^3): one wave per SIMD is all the outputs give at
 // 2x2 per thread, and then the LDS reads of both operands (four values per
-// four fmas, at most one read per ~30 cycles per wave) set the pace.  Here a
-// wave owns RW rows x 64 columns, lane = column.  The workgroup's RW*RWV rows
-// of A are staged in LDS once (K <= ROWS_MAX_K) and read back as broadcasts
-// (every lane the same address, one ds_read_b128 per row per four k).  B is
-// streamed from global memory: per k one coalesced 256-byte row segment, a
-// ring of PB groups of KU rows in flight per wave.  Every output is still one
-// fma chain over k = 0..K-1 in order.  At 512^3: 21.7 us (the 32x32 LDS-tiled
-// kernel 32.6 us); 1 or 4 rows per wave measured 27.1 and 26.8 us.
+// four fmas, at most one read per ~30 cycles per wave) set the pace.  The
+// row kernel instead gives a wave RW rows x 64 columns, lane = column, and
+// stages the workgroup's RW*RWV rows of A in LDS once (K <= kF32RowsMaxK),
+// read back as broadcasts (every lane the same address, one ds_read_b128 per
+// row per four k).  Every output is still one fma chain over k = 0..K-1 in
+// order.
 constexpr int RWV = kF32RowsWaves;     // waves per workgroup (4 x RW rows x 64 columns)
-constexpr int KU = 4;                  // k per group (one ds_read_b128 of A per row)
-constexpr int ROWS_MAX_K = kF32RowsMaxK;  // RW * RWV rows of K floats in LDS: 64 KiB at RW = 2
 
-template <int ACT, int RW>  // RW rows per wave
-__global__ __launch_bounds__(64 * RWV) void gemm_f32_rows_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ bias,
-    float* __restrict__ C, int M, int N, int K) {
-    extern __shared__ float sA[];  // [RW * RWV][Kp]
-    const int Kp = (K + 3) & ~3;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = blockIdx.x * 64 + lane;
-    const int nc = min(n, N - 1);  // columns past N compute on a valid column, never stored
-    const int mb = blockIdx.y * RW * RWV;
-    // stage rows mb .. mb + RW*RWV - 1 of A (rows past M repeat row M-1)
-    for (int i = threadIdx.x; i < RW * RWV * K; i += 64 * RWV) {
-        const int r = i / K, k = i - r * K;
-        sA[r * Kp + k] = A[(int64_t)min(mb + r, M - 1) * K + k];
-    }
-    __syncthreads();
-    const float* arow[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r) arow[r] = sA + (wave * RW + r) * Kp;
-    const float* bcol = B + nc;
-
-    float acc[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
-    // Groups of KU k-steps.  The B row segments of group g+PB are loaded while
-    // group g is computed (a ring of PB groups in registers).  Prefetches past
-    // the last group reload the last group (never used), so every load is
-    // unconditional.  One row per wave (the grids with few waves) keeps 12
-    // groups in flight (48 loads; g1-g3 5-9 % faster than 8), two rows 8
-    // (12 made C1 3 % slower).
-    constexpr int PB = RW == 1 ? 12 : 8;
-    const int ng = K / KU;
-    const int64_t nstride = N;
-    float bq[PB][KU];
-    auto load_b = [&](float(&dst)[KU], int g) {
-        const float* p = bcol + (int64_t)min(g, ng - 1) * KU * nstride;
-#pragma unroll
-        for (int u = 0; u < KU; ++u) dst[u] = p[u * nstride];
-    };
-    // group g: B in ring slot i
-    auto step = [&](int i, int g) {
-        float4 a[RW];
-#pragma unroll
-        for (int r = 0; r < RW; ++r) a[r] = *reinterpret_cast<const float4*>(arow[r] + g * KU);
-#pragma unroll
-        for (int r = 0; r < RW; ++r) {
-            acc[r] = __builtin_fmaf(a[r].x, bq[i][0], acc[r]);
-            acc[r] = __builtin_fmaf(a[r].y, bq[i][1], acc[r]);
-            acc[r] = __builtin_fmaf(a[r].z, bq[i][2], acc[r]);
-            acc[r] = __builtin_fmaf(a[r].w, bq[i][3], acc[r]);
-        }
-        load_b(bq[i], g + PB);
-    };
-    int g = 0;
-    if (ng > 0) {
-#pragma unroll
-        for (int i = 0; i < PB; ++i) load_b(bq[i], i);
-        for (; g + PB <= ng; g += PB) {
-#pragma unroll
-            for (int i = 0; i < PB; ++i) step(i, g + i);
-        }
-        // the last ng % PB groups: group g + i sits in ring slot i (g is a multiple of PB)
-#pragma unroll
-        for (int i = 0; i < PB - 1; ++i)
-            if (g + i < ng) step(i, g + i);
-    }
-    for (int k = ng * KU; k < K; ++k) {
-        const float b = bcol[(int64_t)k * N];
-#pragma unroll
-        for (int r = 0; r < RW; ++r) acc[r] = __builtin_fmaf(arow[r][k], b, acc[r]);
-    }
-    if (n >= N) return;
-    const float bv = bias ? bias[n] : 0.0f;
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const int m = mb + wave * RW + r;
-        if (m >= M) continue;
-        float v = acc[r];
-        if (bias) v = v + bv;
-        C[(int64_t)m * N + n] = activate<ACT>(v);
-    }
-}
-
-
-// ---- row kernel with B streamed through an LDS ring by LDS DMA ----
-// Same work split and fma chains as gemm_f32_rows_kernel (a wave owns RW rows
-// x 64 columns, lane = column, A rows staged in LDS once), but the B column
-// block reaches LDS by LDS DMA through a ring of RD_NST stages of RD_KG k-rows,
-// so the bytes in flight are not bounded by the wave's registers, and the
-// workgroup's four waves share each B row instead of each loading it.  The
+// ---- row kernel: B streamed through an LDS ring by LDS DMA ----
+// The B column block reaches LDS by LDS DMA through a ring of RD_NST stages of
+// RD_KG k-rows, so the bytes in flight are not bounded by the wave's
+// registers, and the workgroup's four waves share each B row (a register
+// ring that each wave filled with its own loads ran C1 in 18.6 us, g2 in 6.7
+// and 300x7x1500 in 30.2 against 16.0 / 5.7 / 24.9 us here).  The
 // LDS reads (A as a broadcast b128 per row, B as 4 b32 per group of 4 k) run
 // RD_PD groups ahead; they are inline asm with explicit waits (through
 // builtins the compiler drains every DMA in flight before any LDS read).
-// Used when N % 4 == 0 and B is 16-byte aligned (16-byte DMA pieces).
+// PIECE = 16 (N % 4 == 0 and B 16-byte aligned): a copy instruction moves 4
+// rows of 64 columns.  PIECE = 4 (any N, B 4-byte aligned): one row per
+// instruction, four times the instructions for the same bytes.
 // At C1 (512^3): 16.0 us against 18.6 us for the register ring; g1 12.8 vs
 // 17.0, g3 9.0 vs 11.9 (32-row stages with 6 stages: 17.6 / 14.8 / 10.2).
 constexpr int RD_KG = 64;   // k rows per ring stage (16 KiB of B)
@@ -260,7 +173,7 @@ __device__ __forceinline__ void rd_wait(f32x4_t (&a)[RW], float (&b)[4]) {
                      : "memory");
 }
 
-template <int ACT, int RW>
+template <int ACT, int RW, int PIECE>
 __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ bias,
     float* __restrict__ C, int M, int N, int K) {
@@ -282,13 +195,17 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
     }
     __syncthreads();
 
-    // stage s of B: rows [32 s, 32 s + 32) x columns [n0, n0 + 64), 8 pieces
-    // of 4 rows (1 KiB); wave w moves pieces 2w and 2w+1.  Lane l of piece i
-    // moves row 4i + l/16, columns n0 + 4(l%16) .. +3.  The buffer covers the
+    // stage s of B: rows [RD_KG s, RD_KG (s + 1)) x columns [n0, n0 + 64) in
+    // CPW instructions per wave.  PIECE 16: instruction i moves rows 4i ..
+    // 4i+3, lane l row 4i + l/16, columns n0 + 4(l%16) .. +3.  PIECE 4:
+    // instruction i moves row i, lane l column n0 + l.  The buffer covers the
     // stage's rows that exist (none past the last stage: no traffic), so every
-    // call issues two instructions and the wait counts are constants.  Columns
+    // call issues CPW instructions and the wait counts are constants.  Columns
     // past N read the next row (or 0 past the end): they only feed outputs
     // that are not stored.
+    static_assert(PIECE == 16 || PIECE == 4, "16- or 4-byte copy pieces");
+    constexpr int RPI = PIECE / 4;             // B rows per copy instruction
+    constexpr int CPW = RD_KG / RPI / RWV;     // copy instructions per wave per stage
     auto copy_stage = [&](int s) {
         const bool live = s < nst;
         const int rows = live ? min(RD_KG, K - RD_KG * s) : 0;
@@ -296,11 +213,16 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
             const_cast<float*>(B) + (int64_t)RD_KG * (live ? s : 0) * N, 0, (uint32_t)rows * (uint32_t)N * 4u,
             0x00020000);
 #pragma unroll
-        for (int p = 0; p < RD_KG / 16; ++p) {
-            const int i = (RD_KG / 16) * wave + p;
-            const uint32_t vo = ((uint32_t)(4 * i + (lane >> 4)) * (uint32_t)N + (uint32_t)(n0 + 4 * (lane & 15))) * 4u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                src, (lds_void_f*)(sB + ((s % RD_NST) * RD_KG + 4 * i) * 64), 16, vo, 0, 0, 0);
+        for (int p = 0; p < CPW; ++p) {
+            const int i = CPW * wave + p;
+            const uint32_t row = (uint32_t)(RPI * i + (PIECE == 16 ? (lane >> 4) : 0));
+            const uint32_t c = (uint32_t)(n0 + (PIECE == 16 ? 4 * (lane & 15) : lane));
+            const uint32_t vo = (row * (uint32_t)N + c) * 4u;
+            lds_void_f* dst = (lds_void_f*)(sB + ((s % RD_NST) * RD_KG + RPI * i) * 64);
+            if constexpr (PIECE == 16)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(src, dst, 16, vo, 0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(src, dst, 4, vo, 0, 0, 0);
         }
     };
 
@@ -313,11 +235,12 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
 #pragma unroll
     for (int p = 0; p < RD_NST - 1; ++p) copy_stage(p);
     for (int s = 0; s < nst; ++s) {
-        // this wave's pieces of stage s have landed once the 2 (RD_NST - 2)
+        // this wave's pieces of stage s have landed once the CPW (RD_NST - 2)
         // instructions of the later stages are all that remain; the barrier
         // makes every wave's pieces visible and ends every wave's reads of
         // stage s - 1, whose slot the next copy reuses
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((RD_KG / 16) * (RD_NST - 2)) : "memory");
+        static_assert(CPW * (RD_NST - 2) <= 63, "vmcnt is a 6-bit count");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPW * (RD_NST - 2)) : "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         copy_stage(s + RD_NST - 1);
@@ -430,30 +353,32 @@ hipError_t launch_gemm_f32_variant(int variant, int act, const float* A, const f
                                    const float* bias, float* C, int M, int N, int K,
                                    hipStream_t s) {
     hipError_t e = hipSuccess;
-    auto rows = [&](auto kern, int rw) {
-        dim3 grid((N + 63) / 64, (M + rw * RWV - 1) / (rw * RWV));
-        const size_t lds = (size_t)rw * RWV * ((K + 3) & ~3) * sizeof(float);
-        hipLaunchKernelGGL(kern, grid, dim3(64 * RWV), lds, s, A, B, bias, C, M, N, K);
-        return hipGetLastError();
-    };
-    const bool dma = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(B) % 16) == 0;
+    // 16-byte copy pieces need whole 16-byte B rows; 4-byte pieces any N
+    const bool p16 = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(B) % 16) == 0;
     auto rowsdma = [&](auto kern, int rw) {
         dim3 grid((N + 63) / 64, (M + rw * RWV - 1) / (rw * RWV));
         const size_t lds = ((size_t)RD_NST * RD_KG * 64 + (size_t)rw * RWV * ((K + 3) & ~3)) * sizeof(float);
         hipLaunchKernelGGL(kern, grid, dim3(64 * RWV), lds, s, A, B, bias, C, M, N, K);
         return hipGetLastError();
     };
-    if (dma && variant == GV_F32_ROWS1) {
-        JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 1>, 1));
-        return e;
-    }
-    if (dma && variant == GV_F32_ROWS2) {
-        JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 2>, 2));
-        return e;
-    }
+    if ((variant == GV_F32_ROWS1 || variant == GV_F32_ROWS2) &&
+        (reinterpret_cast<uintptr_t>(B) % 4) != 0)
+        return hipErrorInvalidValue;  // the C ABI requires 4-byte aligned operands
     switch (variant) {
-    case GV_F32_ROWS1: JH_DISPATCH_ACT(act, ACT, e = rows(gemm_f32_rows_kernel<ACT, 1>, 1)); break;
-    case GV_F32_ROWS2: JH_DISPATCH_ACT(act, ACT, e = rows(gemm_f32_rows_kernel<ACT, 2>, 2)); break;
+    case GV_F32_ROWS1:
+        if (p16) {
+            JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 1, 16>, 1));
+        } else {
+            JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 1, 4>, 1));
+        }
+        break;
+    case GV_F32_ROWS2:
+        if (p16) {
+            JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 2, 16>, 2));
+        } else {
+            JH_DISPATCH_ACT(act, ACT, e = rowsdma(gemm_f32_rowsdma_kernel<ACT, 2, 4>, 2));
+        }
+        break;
     case GV_F32_T32:
         JH_DISPATCH_ACT(act, ACT, e = (run<32, 32, kF32SliceK, 2, 2, ACT>(A, B, bias, C, M, N, K, s)));
         break;

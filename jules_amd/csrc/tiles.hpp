@@ -11,7 +11,8 @@
 // bits.  The variants:
 //   F32_ROWS1 / F32_ROWS2: a wave owns 1 or 2 rows x 64 columns, 4 waves per
 //     workgroup; the workgroup's rows of A (all of K) sit in LDS, so K is
-//     limited to kF32RowsMaxK.  Tile (4*rw) x 64 x K.
+//     limited to kF32RowsMaxK, and B streams through an LDS ring by LDS DMA.
+//     Tile (4*rw) x 64 x K.
 //   F32_T32 / F32_T64: 32x32 (2x2 per thread) and 64x64 (4x4 per thread)
 //     output tiles, A and B staged through LDS in K slices of 32.
 // bf16 (MFMA): 256x256 output tiles of 4 waves; BF16_DMA copies 32-deep K

@@ -52,10 +52,12 @@ def test_f32_shapes_bit_exact(dev, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(5, 21, 7), (33, 50, 19),
-                                   # N % 4 != 0: the row kernel with B in a register ring
-                                   # (the reference's published 64 x 10 x 256 shape); N % 4 == 0
-                                   # with a partial 64-column block: the LDS-DMA ring
-                                   (64, 10, 256), (40, 130, 300), (37, 132, 77)])
+                                   # N % 4 != 0: the row kernel's B ring copied in 4-byte
+                                   # pieces (the reference's published 64 x 10 x 256 shape;
+                                   # several ring stages with K % 4 = 3); N % 4 == 0 with a
+                                   # partial 64-column block: 16-byte pieces
+                                   (64, 10, 256), (40, 130, 300), (50, 33, 259), (300, 7, 1500),
+                                   (37, 132, 77)])
 def test_f32_ragged_n_against_fp64(dev, M, N, K):
     """N not a multiple of 16: the reference's tail columns use libm tanhf;
     the GPU keeps the vector-path activation, so parity is to the fp64 bar."""
