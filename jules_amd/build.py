@@ -72,7 +72,43 @@ def _compile(src, verbose):
         err = "\n".join(l for l in r.stderr.splitlines() if "kernel-resource-usage" not in l)
         if err.strip():
             print(err, file=sys.stderr)
+    if src.endswith(".hip"):
+        _check_lds_waits(src, path, lang, verbose)
     return obj
+
+
+def _isa_check():
+    """isa_check.py beside this file, loaded by path (this script also runs
+    outside the package, and the package's own import loads the library)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("jules_isa_check", os.path.join(HERE, "isa_check.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _check_lds_waits(src, path, lang, verbose):
+    """The same source as gfx950 assembly, checked by isa_check: no register
+    an LDS read is still filling may be read, copied or reused before the
+    wait that covers it (the asm-issued reads are invisible to the
+    compiler's own waits)."""
+    check_asm = _isa_check().check_asm
+
+    asm = os.path.join(OBJDIR, src + ".s")
+    cmd = [HIPCC, *COMMON, *DEVICE, *lang, "--cuda-device-only", "-S", path, "-o", asm]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src}:\n{r.stdout}\n{r.stderr}")
+    with open(asm) as fh:
+        bad = check_asm(fh.read())
+    if bad:
+        lines = [f"  {k[:70]}: line {ln}: {t}" for k, v in bad.items() for ln, t in v[:3]]
+        raise RuntimeError(f"{src}: instructions touch registers an LDS read is still "
+                           f"filling ({sum(len(v) for v in bad.values())} found):\n" +
+                           "\n".join(lines))
 
 
 def build(verbose: bool = False, jobs: int = 8) -> str:

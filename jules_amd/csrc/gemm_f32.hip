@@ -127,7 +127,7 @@ constexpr int RWV = kF32RowsWaves;     // waves per workgroup (4 x RW rows x 64 
 // registers, and the workgroup's four waves share each B row (a register
 // ring that each wave filled with its own loads ran C1 in 18.6 us, g2 in 6.7
 // and 300x7x1500 in 30.2 against 16.0 / 5.7 / 24.9 us here).  The
-// LDS reads (A as a broadcast b128 per row, B as 4 b32 per group of 4 k) run
+// LDS reads (A as a broadcast b128 per row, B as two read2 per group of 4 k) run
 // RD_PD groups ahead; they are inline asm with explicit waits (through
 // builtins the compiler drains every DMA in flight before any LDS read).
 // PIECE = 16 (N % 4 == 0 and B 16-byte aligned): a copy instruction moves 4
@@ -153,6 +153,14 @@ __device__ __forceinline__ float rd_f32(uint32_t a) {
     asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF) : "memory");
     return v;
 }
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+// two dwords 256 * O0 and 256 * O1 bytes past a (B rows O0 and O1 of a group)
+template <int O0, int O1>
+__device__ __forceinline__ f32x2_t rd_f32x2_st64(uint32_t a) {
+    f32x2_t v;
+    asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(v) : "v"(a), "n"(O0), "n"(O1) : "memory");
+    return v;
+}
 template <int OFF>
 __device__ __forceinline__ f32x4_t rd_f128(uint32_t a) {
     f32x4_t v;
@@ -163,14 +171,12 @@ __device__ __forceinline__ f32x4_t rd_f128(uint32_t a) {
 // Waits until at most N LDS reads are outstanding; the group's operands pass
 // through the asm, so no fma that uses them is scheduled above the wait.
 template <int N, int RW>
-__device__ __forceinline__ void rd_wait(f32x4_t (&a)[RW], float (&b)[4]) {
+__device__ __forceinline__ void rd_wait(f32x4_t (&a)[RW], f32x2_t (&b)[2]) {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt is a 4-bit count");
     if constexpr (RW == 1)
-        asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(a[0]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]) : "n"(N) : "memory");
+        asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a[0]), "+v"(b[0]), "+v"(b[1]) : "n"(N) : "memory");
     else
-        asm volatile("s_waitcnt lgkmcnt(%6)"
-                     : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])
-                     : "n"(N)
-                     : "memory");
+        asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]) : "n"(N) : "memory");
 }
 
 template <int ACT, int RW, int PIECE>
@@ -248,18 +254,18 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
         const int k0 = RD_KG * s;
         const uint32_t bs = b0 + (uint32_t)((s % RD_NST) * RD_KG * 64 * 4);
         const int ng = kv >> 2;
-        // groups of 4 k: A as one b128 per row, B as 4 b32; a ring of RD_PD
-        // groups of reads in flight
+        // groups of 4 k: A as one b128 per row, B as two ds_read2st64_b32 (rows
+        // 0-1 and 2-3 of the group, 256 bytes apart); a ring of RD_PD groups of
+        // reads in flight.  The pairs stay whole until their wait, so no copy of
+        // a register still being filled is scheduled before it.
         f32x4_t a[RD_PD][RW];
-        float b[RD_PD][4];
+        f32x2_t b[RD_PD][2];  // B rows 0-1 and 2-3 of the group
         auto rd = [&](int g, int slot) {
 #pragma unroll
             for (int r = 0; r < RW; ++r) a[slot][r] = rd_f128<0>(a0 + (uint32_t)((r * Kp + k0 + 4 * g) * 4));
             const uint32_t bg = bs + (uint32_t)(4 * g * 64 * 4);
-            b[slot][0] = rd_f32<0>(bg);
-            b[slot][1] = rd_f32<256>(bg);
-            b[slot][2] = rd_f32<512>(bg);
-            b[slot][3] = rd_f32<768>(bg);
+            b[slot][0] = rd_f32x2_st64<0, 1>(bg);
+            b[slot][1] = rd_f32x2_st64<2, 3>(bg);
         };
         if (ng == RD_KG / 4) {
             // a full stage: fully unrolled, compile-time ring slots and waits
@@ -268,13 +274,13 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
             static_for_f<0, NG>([&](auto ic) {
                 constexpr int g = decltype(ic)::value, slot = g % RD_PD;
                 constexpr int later = (g + RD_PD - 1 < NG ? RD_PD - 1 : NG - 1 - g);  // groups read after g
-                rd_wait<later * (RW + 4), RW>(a[slot], b[slot]);
+                rd_wait<later * (RW + 2), RW>(a[slot], b[slot]);
 #pragma unroll
                 for (int r = 0; r < RW; ++r) {
-                    acc[r] = __builtin_fmaf(a[slot][r].x, b[slot][0], acc[r]);
-                    acc[r] = __builtin_fmaf(a[slot][r].y, b[slot][1], acc[r]);
-                    acc[r] = __builtin_fmaf(a[slot][r].z, b[slot][2], acc[r]);
-                    acc[r] = __builtin_fmaf(a[slot][r].w, b[slot][3], acc[r]);
+                    acc[r] = __builtin_fmaf(a[slot][r].x, b[slot][0].x, acc[r]);
+                    acc[r] = __builtin_fmaf(a[slot][r].y, b[slot][0].y, acc[r]);
+                    acc[r] = __builtin_fmaf(a[slot][r].z, b[slot][1].x, acc[r]);
+                    acc[r] = __builtin_fmaf(a[slot][r].w, b[slot][1].y, acc[r]);
                 }
                 if constexpr (g + RD_PD < NG) rd(g + RD_PD, slot);
             });
@@ -285,10 +291,10 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
                 rd_wait<0, RW>(a[0], b[0]);
 #pragma unroll
                 for (int r = 0; r < RW; ++r) {
-                    acc[r] = __builtin_fmaf(a[0][r].x, b[0][0], acc[r]);
-                    acc[r] = __builtin_fmaf(a[0][r].y, b[0][1], acc[r]);
-                    acc[r] = __builtin_fmaf(a[0][r].z, b[0][2], acc[r]);
-                    acc[r] = __builtin_fmaf(a[0][r].w, b[0][3], acc[r]);
+                    acc[r] = __builtin_fmaf(a[0][r].x, b[0][0].x, acc[r]);
+                    acc[r] = __builtin_fmaf(a[0][r].y, b[0][0].y, acc[r]);
+                    acc[r] = __builtin_fmaf(a[0][r].z, b[0][1].x, acc[r]);
+                    acc[r] = __builtin_fmaf(a[0][r].w, b[0][1].y, acc[r]);
                 }
             }
         }
