@@ -106,13 +106,6 @@ __device__ __forceinline__ void load_tile(uint8_t* tile, const uint16_t* __restr
     }
 }
 
-// A/B fragment: 8 consecutive head-dim elements of one row (16 bytes)
-template <int D>
-__device__ __forceinline__ bf16x8_t row_frag(const uint8_t* tile, int row, int ks, int g) {
-    return as_bf16x8(*reinterpret_cast<const u32x4_t*>(tile + row * BwdCfg<D>::PITCH +
-                                                       (16 * ks + 8 * g) * 2));
-}
-
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
     if constexpr (I < N) {
@@ -177,6 +170,28 @@ __device__ __forceinline__ void tr_pipeline(uint32_t base, O&& off, U&& use) {
         constexpr int later = (m + L < NM ? L : NM - 1 - m);  // MFMAs whose reads follow m's
         use(mi, tr_wait<2 * later>(ring[m % R]));
     });
+}
+
+// A/B fragment of the S and dP products: 8 consecutive head-dim elements of
+// one row (16 bytes), read by inline asm at a compile-time byte offset and
+// waited for with row_wait (the compiler's own schedule waited on every read
+// right before its MFMA)
+template <int OFF>
+__device__ __forceinline__ u32x4_t row_issue(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "16-bit LDS offset");
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+template <int N>
+__device__ __forceinline__ void row_wait1(u32x4_t& a) {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt is a 4-bit count");
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void row_wait2(u32x4_t& a, u32x4_t& b) {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt is a 4-bit count");
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
 }
 
 __device__ __forceinline__ f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
@@ -309,13 +324,25 @@ __global__ __launch_bounds__(BT, 2) void flash_bwd_dkdv_kernel(
 #pragma unroll
         for (int h = 0; h < 1; ++h) {
             f32x16_t s = zero16(), dp = zero16();
-            // (compiler-scheduled reads: a read pipeline here needs registers
-            // this kernel does not have at two waves per SIMD)
-#pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
-                s = mfma(row_frag<D>(q_t, h * 32 + col, ks, g), kf[ks], s);
-                dp = mfma(row_frag<D>(do_t, h * 32 + col, ks, g), row_frag<D>(v_t, vrow, ks, g), dp);
-            }
+            // each MFMA's fragments are read one MFMA ahead (inline asm with
+            // explicit waits; one register set per operand)
+            const uint32_t qa = (uint32_t)(uintptr_t)(q_t + (h * 32 + col) * C::PITCH + 16 * g);
+            const uint32_t da = (uint32_t)(uintptr_t)(do_t + (h * 32 + col) * C::PITCH + 16 * g);
+            const uint32_t va = (uint32_t)(uintptr_t)(v_t + vrow * C::PITCH + 16 * g);
+            u32x4_t rq = row_issue<0>(qa), rd = row_issue<0>(da), rv = row_issue<0>(va);
+            static_for<0, C::KS>([&](auto ksc) {
+                constexpr int ks = decltype(ksc)::value;
+                constexpr bool more = ks + 1 < C::KS;
+                row_wait1<2>(rq);  // dO(ks), V(ks) may still be in flight
+                s = mfma(as_bf16x8(rq), kf[ks], s);
+                if constexpr (more) rq = row_issue<32 * (ks + 1)>(qa);
+                row_wait2<more ? 1 : 0>(rd, rv);  // Q(ks+1) may still be in flight
+                dp = mfma(as_bf16x8(rd), as_bf16x8(rv), dp);
+                if constexpr (more) {
+                    rd = row_issue<32 * (ks + 1)>(da);
+                    rv = row_issue<32 * (ks + 1)>(va);
+                }
+            });
             // register r: query 8(r/4) + 4g + r%4 of this block.  Every step
             // computes P and dS unmasked; only the last block and the
             // diagonal then zero the masked elements (queries past S, causal
