@@ -94,6 +94,9 @@ __device__ __forceinline__ void block_coords(int BH, int nq, int bq, int* bh, in
 //               moved), P_j = exp2(S_j c - m) packed to bf16, row sums.
 //   group A: MFMA(j) in phase 2j,     SOFTMAX(j) in phase 2j+1;
 //   group B: MFMA(j) in phase 2j+1,   SOFTMAX(j) in phase 2j+2.
+// At D = 128 only the barriers after odd phases are kept (one per key tile):
+// each group runs its two halves of a tile back to back and the groups meet
+// once per tile, still half a tile apart.
 //
 // K and V tiles of 64 keys go HBM -> LDS by the LDS DMA path
 // (global_load_lds_dwordx4: each lane's 16 bytes land at base + 16 * lane)
