@@ -220,8 +220,8 @@ __global__ __launch_bounds__(512, 1) void flash_bwd_dq_pp_kernel(
     // masked), and every offset stays small whatever S is ----
     const uint32_t sm0 = (uint32_t)(uintptr_t)sm;
     auto dma_part = [&](int t, int p0, int p1) {
-        const int64_t tr0 = (int64_t)t * DQ_BKV;
-        const uint32_t bytes = (uint32_t)min(DQ_BKV, S - t * DQ_BKV) * (uint32_t)C::ROW;
+        const int64_t tr0 = (int64_t)min(t * DQ_BKV, S);  // a tile past the end: an empty range at S
+        const uint32_t bytes = (uint32_t)max(0, min(DQ_BKV, S - t * DQ_BKV)) * (uint32_t)C::ROW;
         const __amdgpu_buffer_rsrc_t ksrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(Kh + tr0 * D), 0, bytes, 0x00020000);
         const __amdgpu_buffer_rsrc_t vsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -367,9 +367,13 @@ __global__ __launch_bounds__(512, 1) void flash_bwd_dq_pp_kernel(
     auto need = [&](int u) { return 32 * u < S && (!CAUSAL || 32 * u <= qw0 + 31); };
 
     // ---- prologue: Q, dO, lse, dvec and tiles 0, 1 in flight; wait for all but tile 1 ----
+    // tile 1 is copied even when there is no tile 1 (an empty buffer range:
+    // no traffic, into a stage nothing reads), so the wait count is one
+    // constant on every path: the static ISA check cannot correlate two
+    // branches on n_t
     dma_part(0, 0, PIECES);
-    if (n_t > 1) dma_part(1, 0, PIECES);
-    dq_vm(n_t > 1 ? PIECES : 0);
+    dma_part(1, 0, PIECES);
+    dq_vm(PIECES);
     dq_barrier();
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {

@@ -472,8 +472,11 @@ __device__ __forceinline__ void flash_bf16_body(
 
     // ---- prologue: Q, tiles 0 and 1 in flight; wait for Q and tile 0 ----
     dma_tile(0);
-    if (n_kv > 1) dma_tile(1);
-    vm_wait(n_kv > 1 ? PIECES : 0);
+    // tile 1 is copied even when there is no tile 1 (its rows clamp to S-1 and
+    // land in a stage nothing reads), so the wait count is one constant on
+    // every path: the static ISA check cannot correlate two branches on n_kv
+    dma_tile(1);
+    vm_wait(PIECES);
     bare_barrier();
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
