@@ -57,6 +57,8 @@ def test_f32_shapes_bit_exact(dev, M, N, K):
                                    # several ring stages with K % 4 = 3); N % 4 == 0 with a
                                    # partial 64-column block: 16-byte pieces
                                    (64, 10, 256), (40, 130, 300), (50, 33, 259), (300, 7, 1500),
+                                   # enough waves for 2 rows per wave, N % 4 != 0
+                                   (2048, 130, 100),
                                    (37, 132, 77)])
 def test_f32_ragged_n_against_fp64(dev, M, N, K):
     """N not a multiple of 16: the reference's tail columns use libm tanhf;
