@@ -18,11 +18,13 @@
 // per workgroup), one 1024-thread workgroup per row for N <= 32768.  With
 // N % 4 == 0 and 16-byte aligned rows each thread moves 16-byte pieces,
 // otherwise single floats; either way every wave instruction covers
-// contiguous bytes.  Rows longer than 32768 get a 256-thread workgroup and
-// three passes over the row (max, sum, write: the reference's own pass
-// structure, the exponentials recomputed in the last pass).  Reductions are a
-// fixed butterfly within a wave and a fixed tree across waves, so results
-// are deterministic.
+// contiguous bytes.  Rows longer than 32768 get a 1024-thread workgroup that
+// streams the row three times in chunks of 16 elements per thread, in the
+// reference's own passes (softmax and cross entropy: max, sum of
+// exponentials, write with the exponentials recomputed; layernorm: sum,
+// squared deviations, write); the later passes mostly find the row in the
+// caches.  Reductions are a fixed butterfly within a wave and a fixed tree
+// across waves, so results are deterministic.
 #include <cfloat>
 
 #include "common.hpp"
@@ -219,45 +221,113 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void softmax_ke
     R.store(out + (int64_t)row * N, N, tid);
 }
 
-// ---- rows longer than a block holds: one 256-thread workgroup per row,
-// three passes ----
-constexpr int LT = 256;  // threads per long row
+// ---- rows longer than a block holds: one BT-thread workgroup per row, the
+// row streamed in chunks of LCH elements, LE per thread (16-byte accesses
+// under the same conditions as the held rows, else single floats) ----
+constexpr int LE = 16;          // elements per thread per chunk (its loads in flight)
+constexpr int LCH = BT * LE;    // elements per chunk
 
-// f(j) for j = tid, tid + 256, ... < N, four loads in flight
-template <typename F>
-__device__ __forceinline__ void row_loop(int N, F&& f) {
-    int j = threadIdx.x;
-    for (; j + 3 * LT < N; j += 4 * LT) {
-        f(j);
-        f(j + LT);
-        f(j + 2 * LT);
-        f(j + 3 * LT);
+template <bool VEC>
+struct Chunk {
+    static constexpr int W = VEC ? 4 : 1;
+    static constexpr int NA = LE / W;
+    float v[LE];
+    // offset in the chunk of this thread's access a, element i; a chunk
+    // starts at a multiple of LCH, so element j of the row belongs to thread
+    // (VEC ? j / 4 : j) % BT
+    __device__ __forceinline__ static int off(int a, int i) {
+        return VEC ? 4 * ((int)threadIdx.x + BT * a) + i : (int)threadIdx.x + BT * a;
     }
-    for (; j < N; j += LT) f(j);
+    // v[] = x[0 .. rem) of the chunk starting at x, pad past it (rem > 0;
+    // with VEC rem % 4 == 0)
+    __device__ __forceinline__ void load(const float* x, int rem, float pad) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const int o = off(a, 0);
+            if constexpr (VEC) {
+                f32x4_t q = {pad, pad, pad, pad};
+                if (o < rem) q = *reinterpret_cast<const f32x4_t*>(x + o);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[4 * a + i] = q[i];
+            } else {
+                v[a] = o < rem ? x[o] : pad;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float* y, int rem) const {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const int o = off(a, 0);
+            if (o < rem) {
+                if constexpr (VEC) {
+                    const f32x4_t q = {v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
+                    *reinterpret_cast<f32x4_t*>(y + o) = q;
+                } else {
+                    y[o] = v[a];
+                }
+            }
+        }
+    }
+    // f(offset in the chunk, value, inside the row)
+    template <typename F>
+    __device__ __forceinline__ void each(int rem, F&& f) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+                const int o = off(a, i);
+                f(o, v[W * a + i], o < rem);
+            }
+    }
+};
+
+// f(chunk start b, elements left rem) over the chunks of a row of N
+template <typename F>
+__device__ __forceinline__ void chunks(int N, F&& f) {
+    for (int64_t b = 0; b < N; b += LCH) f((int)b, (int)(N - b));
 }
 
-// max and sum of exp(x - max) of a long row (reference passes 1a and 1b)
+// row max, then the sum of exp(x - max) (reference passes 1a and 1b), each
+// streaming the row
+template <bool VEC>
 __device__ __forceinline__ void long_row_stats(const float* x, int N, float* red, float* mx_out,
                                                float* s_out) {
     const int nv = N & ~15;
     float mx = -FLT_MAX;
-    row_loop(N, [&](int j) { mx = ref_max(mx, x[j]); });
-    mx = group_max<LT>(mx, red);
+    chunks(N, [&](int b, int rem) {
+        Chunk<VEC> C;
+        C.load(x + b, rem, -FLT_MAX);
+#pragma unroll
+        for (int k = 0; k < LE; ++k) mx = ref_max(mx, C.v[k]);
+    });
+    mx = group_max<BT>(mx, red);
     float s = 0.0f;
-    row_loop(N, [&](int j) { s += row_exp(x[j] - mx, j, nv); });
+    chunks(N, [&](int b, int rem) {
+        Chunk<VEC> C;
+        C.load(x + b, rem, 0.0f);
+        C.each(rem, [&](int o, float e, bool in) { s += in ? row_exp(e - mx, b + o, nv) : 0.0f; });
+    });
     *mx_out = mx;
-    *s_out = group_sum<LT>(s, red);
+    *s_out = group_sum<BT>(s, red);
 }
 
-__global__ __launch_bounds__(LT) void softmax_long_kernel(float* out, const float* in, int N) {
-    __shared__ float red[LT / 64];
+template <bool VEC>
+__global__ __launch_bounds__(BT) void softmax_long_kernel(float* out, const float* in, int N) {
+    __shared__ float red[BT / 64];
     const float* x = in + (int64_t)blockIdx.x * N;
     float* y = out + (int64_t)blockIdx.x * N;
     const int nv = N & ~15;
     float mx, s;
-    long_row_stats(x, N, red, &mx, &s);
+    long_row_stats<VEC>(x, N, red, &mx, &s);
     const float inv = 1.0f / s;
-    row_loop(N, [&](int j) { y[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv); });
+    chunks(N, [&](int b, int rem) {
+        Chunk<VEC> C;
+        C.load(x + b, rem, 0.0f);
+        C.each(rem, [&](int o, float& e, bool) {
+            e = row_norm(row_exp(e - mx, b + o, nv), inv, s, b + o, nv);
+        });
+        C.store(y + b, rem);
+    });
 }
 
 // ---- layernorm ----
@@ -301,24 +371,44 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void layernorm_
     }
 }
 
-__global__ __launch_bounds__(LT) void layernorm_long_kernel(float* out, const float* in,
+// rows longer than a block holds: the reference's three passes (sum, sum of
+// squared deviations, write), each streaming the row in chunks
+template <bool VEC>
+__global__ __launch_bounds__(BT) void layernorm_long_kernel(float* out, const float* in,
                                                            const float* __restrict__ gamma,
                                                            const float* __restrict__ beta, int N,
                                                            float eps) {
-    __shared__ float red[LT / 64];
+    __shared__ float red[BT / 64];
     const float* x = in + (int64_t)blockIdx.x * N;
     float* y = out + (int64_t)blockIdx.x * N;
     float s = 0.0f;
-    row_loop(N, [&](int j) { s += x[j]; });
-    const float mean = group_sum<LT>(s, red) / (float)N;
-    float q = 0.0f;
-    row_loop(N, [&](int j) {
-        const float d = x[j] - mean;
-        q = __builtin_fmaf(d, d, q);
+    chunks(N, [&](int b, int rem) {
+        Chunk<VEC> C;
+        C.load(x + b, rem, 0.0f);
+#pragma unroll
+        for (int k = 0; k < LE; ++k) s += C.v[k];
     });
-    const float var = group_sum<LT>(q, red) / (float)N;
+    const float mean = group_sum<BT>(s, red) / (float)N;
+    float q = 0.0f;
+    chunks(N, [&](int b, int rem) {
+        Chunk<VEC> C;
+        C.load(x + b, rem, 0.0f);
+        C.each(rem, [&](int, float e, bool in) {
+            const float d = e - mean;
+            q = in ? __builtin_fmaf(d, d, q) : q;
+        });
+    });
+    const float var = group_sum<BT>(q, red) / (float)N;
     const float inv_std = 1.0f / sqrtf(var + eps);
-    row_loop(N, [&](int j) { y[j] = __builtin_fmaf((x[j] - mean) * inv_std, gamma[j], beta[j]); });
+    chunks(N, [&](int b, int rem) {
+        Chunk<VEC> C, G, B;
+        C.load(x + b, rem, 0.0f);
+        G.load(gamma + b, rem, 0.0f);
+        B.load(beta + b, rem, 0.0f);
+#pragma unroll
+        for (int k = 0; k < LE; ++k) C.v[k] = __builtin_fmaf((C.v[k] - mean) * inv_std, G.v[k], B.v[k]);
+        C.store(y + b, rem);
+    });
 }
 
 // ---- cross entropy: grad rows and per-row losses (row_loss[M]) ----
@@ -369,10 +459,11 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void cross_entr
     }
 }
 
-__global__ __launch_bounds__(LT) void cross_entropy_long_kernel(const float* logits,
+template <bool VEC>
+__global__ __launch_bounds__(BT) void cross_entropy_long_kernel(const float* logits,
                                                                const int32_t* targets, float* grad,
                                                                float* row_loss, int M, int N) {
-    __shared__ float red[LT / 64];
+    __shared__ float red[BT / 64];
     const int row = blockIdx.x;
     const float* x = logits + (int64_t)row * N;
     float* g = grad + (int64_t)row * N;
@@ -380,17 +471,22 @@ __global__ __launch_bounds__(LT) void cross_entropy_long_kernel(const float* log
     float mx, s;
     const int t = targets[row];
     const bool valid = t >= 0 && t < N;
-    const bool owner = valid && (int)threadIdx.x == t % LT;  // row_loop's owner of element t
+    const bool owner = valid && (int)threadIdx.x == (VEC ? t >> 2 : t) % BT;  // Chunk's owner of t
     const float xt = owner ? x[t] : 0.0f;  // before any store of this row (grad may alias logits)
-    long_row_stats(x, N, red, &mx, &s);
+    long_row_stats<VEC>(x, N, red, &mx, &s);
     const float inv = 1.0f / s;
     const float fm = (float)M;
-    if ((M & (M - 1)) == 0) {  // exact product with 1/M, as in cross_entropy_kernel
-        const float rm = 1.0f / fm;
-        row_loop(N, [&](int j) { g[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv) * rm; });
-    } else {
-        row_loop(N, [&](int j) { g[j] = row_norm(row_exp(x[j] - mx, j, nv), inv, s, j, nv) / fm; });
-    }
+    const bool pow2 = (M & (M - 1)) == 0;  // exact product with 1/M, as in cross_entropy_kernel
+    const float rm = 1.0f / fm;
+    chunks(N, [&](int b, int rem) {
+        Chunk<VEC> C;
+        C.load(x + b, rem, 0.0f);
+        C.each(rem, [&](int o, float& e, bool) {
+            const float p = row_norm(row_exp(e - mx, b + o, nv), inv, s, b + o, nv);
+            e = pow2 ? p * rm : p / fm;
+        });
+        C.store(g + b, rem);
+    });
     if (owner) {
         const float pt = row_norm(row_exp(xt - mx, t, nv), inv, s, t, nv);
         g[t] = (pt - 1.0f) / fm;  // after this thread's own store of g[t]
@@ -490,7 +586,10 @@ unsigned row_blocks(int M) {
 hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t s) {
     if (M == 0) return hipSuccess;
     if (N > MAX_BLOCK_CACHED) {
-        hipLaunchKernelGGL(softmax_long_kernel, dim3(M), dim3(LT), 0, s, out, in, N);
+        if (rows_vec4(N, {out, in}))
+            hipLaunchKernelGGL(softmax_long_kernel<true>, dim3(M), dim3(BT), 0, s, out, in, N);
+        else
+            hipLaunchKernelGGL(softmax_long_kernel<false>, dim3(M), dim3(BT), 0, s, out, in, N);
         return hipGetLastError();
     }
     return by_size(N, rows_vec4(N, {out, in}), [&](auto g, auto e, auto v, auto f) {
@@ -506,8 +605,12 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
                             int M, int N, float eps, hipStream_t s) {
     if (M == 0) return hipSuccess;
     if (N > MAX_BLOCK_CACHED) {
-        hipLaunchKernelGGL(layernorm_long_kernel, dim3(M), dim3(LT), 0, s, out, in, gamma, beta, N,
-                           eps);
+        if (rows_vec4(N, {out, in, gamma, beta}))
+            hipLaunchKernelGGL(layernorm_long_kernel<true>, dim3(M), dim3(BT), 0, s, out, in, gamma,
+                               beta, N, eps);
+        else
+            hipLaunchKernelGGL(layernorm_long_kernel<false>, dim3(M), dim3(BT), 0, s, out, in, gamma,
+                               beta, N, eps);
         return hipGetLastError();
     }
     return by_size(N, rows_vec4(N, {out, in, gamma, beta}), [&](auto g, auto e, auto v, auto) {
@@ -524,8 +627,12 @@ hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, flo
     hipError_t e = hipSuccess;
     if (M > 0) {
         if (N > MAX_BLOCK_CACHED) {
-            hipLaunchKernelGGL(cross_entropy_long_kernel, dim3(M), dim3(LT), 0, s, logits, targets,
-                               grad, row_loss, M, N);
+            if (rows_vec4(N, {logits, grad}))
+                hipLaunchKernelGGL(cross_entropy_long_kernel<true>, dim3(M), dim3(BT), 0, s, logits,
+                                   targets, grad, row_loss, M, N);
+            else
+                hipLaunchKernelGGL(cross_entropy_long_kernel<false>, dim3(M), dim3(BT), 0, s, logits,
+                                   targets, grad, row_loss, M, N);
             e = hipGetLastError();
         } else {
             e = by_size(N, rows_vec4(N, {logits, grad}), [&](auto g, auto el, auto v, auto f) {
