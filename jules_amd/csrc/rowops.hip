@@ -15,17 +15,18 @@
 //
 // All three are HBM-bound, and the row is held in registers so it is read
 // from HBM once and written once: one wave per row for N <= 4096 (four rows
-// per workgroup), one 1024-thread workgroup per row for N <= 32768.  With
-// N % 4 == 0 and 16-byte aligned rows each thread moves 16-byte pieces,
-// otherwise single floats; either way every wave instruction covers
-// contiguous bytes.  Rows longer than 32768 get a 1024-thread workgroup that
-// streams the row three times in chunks of 16 elements per thread, in the
-// reference's own passes (softmax and cross entropy: max, sum of
-// exponentials, write with the exponentials recomputed; layernorm: sum,
-// squared deviations, write); the later passes mostly find the row in the
-// caches.  Reductions are a fixed butterfly within a wave and a fixed tree
-// across waves, so results are deterministic.
+// per workgroup), one 1024-thread workgroup per row for N <= 65536 (up to 64
+// elements per thread).  With N % 4 == 0 and 16-byte aligned rows each
+// thread moves 16-byte pieces, otherwise single floats; either way every wave
+// instruction covers contiguous bytes.  Rows longer than 65536 get a
+// 1024-thread workgroup that streams the row three times in chunks of 16
+// elements per thread, in the reference's own passes (softmax and cross
+// entropy: max, sum of exponentials, write with the exponentials recomputed;
+// layernorm: sum, squared deviations, write); the later passes mostly find
+// the row in the caches.  Reductions are a fixed butterfly within a wave and
+// a fixed tree across waves, so results are deterministic.
 #include <cfloat>
+#include <type_traits>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -36,16 +37,33 @@ namespace {
 constexpr int ROWS_PER_BLOCK = 4;
 constexpr int MAX_CACHED = 4096;      // longest row held in one wave's registers
 constexpr int BT = 1024;              // threads of a block that holds one row
-constexpr int MAX_BLOCK_CACHED = 32768;  // longest row held in a block's registers
+constexpr int MAX_BLOCK_CACHED = 65536;  // longest row held in a block's registers
 
+// Butterfly over the wave's 64 lanes: v of lane ^ o for o = 32, 16, .., 1.
+// The lane id passes through an empty asm at each reduction, so the six
+// permute addresses are rebuilt there (two instructions each) instead of
+// being kept live between a row's reductions, where they would be spilled in
+// the kernels that hold 64 elements per thread.
+__device__ __forceinline__ int fresh_lane() {
+    int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(lane));
+    return lane;
+}
+__device__ __forceinline__ float lane_xor(float v, int lane, int o) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ o) << 2, __builtin_bit_cast(int, v)));
+}
+// the wave's index in the workgroup, in a scalar register
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
 __device__ __forceinline__ float wave_max(float v) {
+    const int lane = fresh_lane();
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, lane_xor(v, lane, o));
     return v;
 }
 __device__ __forceinline__ float wave_sum(float v) {
+    const int lane = fresh_lane();
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int o = 32; o > 0; o >>= 1) v += lane_xor(v, lane, o);
     return v;
 }
 // max as the reference's _mm512_max_ps(acc, x): acc > x ? acc : x
@@ -64,42 +82,98 @@ __device__ __forceinline__ float row_norm(float e, float inv, float sum, int j, 
 // the BT threads of a block).  Thread `tid` holds ELEMS elements: with VEC,
 // 16-byte pieces f = tid + G*t, elements 4f .. 4f+3 (rows 16-byte aligned,
 // N % 4 == 0); without, elements j = tid + G*t.  Every load or store
-// instruction of a wave covers contiguous bytes. ----
+// instruction of a wave covers contiguous bytes.
+// The BT-thread rows use range-checked buffer accesses over the row (N * 4
+// bytes, N <= 65536): a store past the row's end is dropped without a
+// branch, and at 64 elements per thread the kernels fit in 128 registers.
+// One wave per row uses plain global accesses, which measured 3-13 % faster
+// there (many short rows per CU); a row's stores all take the same kind of
+// access, so the same thread's later store to an address lands last. ----
 template <int G, int ELEMS, bool VEC>
 struct RowRegs {
     static constexpr int W = VEC ? 4 : 1;   // elements per access
     static constexpr int NA = ELEMS / W;    // accesses per thread
+    static constexpr bool BUF = G != 64;
+    using Access = std::conditional_t<VEC, f32x4_t, float>;
     float v[ELEMS];
     __device__ __forceinline__ static int elem(int tid, int a, int i) {
         return VEC ? 4 * (tid + G * a) + i : tid + G * a;
     }
-    // v[] = x[] (pad outside the row)
-    __device__ __forceinline__ void load(const float* __restrict__ x, int N, int tid, float pad) {
+    // access a of the group's threads covers elements [first(a), first(a + 1))
+    static constexpr int first(int a) { return G * W * a; }
+    // byte offset of this thread's access 0; access a adds 4 * first(a).  The
+    // stores take it through an empty asm, so the compiler rebuilds their
+    // offsets instead of keeping every load's offset live until the stores.
+    __device__ __forceinline__ static uint32_t base_off(int tid) { return (uint32_t)elem(tid, 0, 0) * 4u; }
+    __device__ __forceinline__ static uint32_t fresh_base_off(int tid) {
+        uint32_t o = base_off(tid);
+        asm volatile("" : "+v"(o));
+        return o;
+    }
+    __device__ __forceinline__ static __amdgpu_buffer_rsrc_t row_rsrc(const float* p, int N) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, (uint32_t)N * 4u,
+                                                 0x00020000);
+    }
+    // one access of the row p at byte offset o (o + 4 W <= N * 4)
+    __device__ __forceinline__ static Access load_at(const float* p, __amdgpu_buffer_rsrc_t src,
+                                                     uint32_t o) {
+        if constexpr (BUF) {
+            if constexpr (VEC)
+                return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src, o, 0, 0));
+            else
+                return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src, o, 0, 0));
+        } else {
+            return *reinterpret_cast<const Access*>(reinterpret_cast<const char*>(p) + o);
+        }
+    }
+    // one access stored at byte offset o; nothing if o is past the row
+    __device__ __forceinline__ static void store_at(float* p, __amdgpu_buffer_rsrc_t dst, int N,
+                                                    uint32_t o, Access q) {
+        if constexpr (BUF) {
+            if constexpr (VEC)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, q), dst, o, 0, 0);
+            else
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, q), dst, o, 0, 0);
+        } else if (o < (uint32_t)N * 4u) {
+            *reinterpret_cast<Access*>(reinterpret_cast<char*>(p) + o) = q;
+        }
+    }
+    // v[] = x[]; past the row's end, with LAST the row's last element (piece,
+    // with VEC) again, else 0.  LAST leaves the row's max unchanged without a
+    // select per element (in the BT-thread rows a compare per element held
+    // until its load lands costs a pair of scalar registers each).  The
+    // offsets are clamped into the row; the buffer form reads 0 past it.
+    template <bool LAST>
+    __device__ __forceinline__ void load(const float* x, int N, int tid) {
+        const __amdgpu_buffer_rsrc_t src = row_rsrc(x, N);
+        const uint32_t o0 = base_off(tid);
+        const uint32_t last = (uint32_t)(N - W) * 4u;  // N >= W: with VEC, N % 4 == 0
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
-            const int j0 = elem(tid, a, 0);
+            const uint32_t o = o0 + 4u * (uint32_t)first(a);
+            Access q = load_at(x, src, (LAST || !BUF) ? (o < last ? o : last) : o);
+            if constexpr (!LAST && !BUF) q = o <= last ? q : Access{};
             if constexpr (VEC) {
-                f32x4_t q = {pad, pad, pad, pad};
-                if (j0 < N) q = *reinterpret_cast<const f32x4_t*>(x + j0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[4 * a + i] = q[i];
             } else {
-                v[a] = j0 < N ? x[j0] : pad;
+                v[a] = q;
             }
         }
     }
-    __device__ __forceinline__ void store(float* __restrict__ y, int N, int tid) const {
+    // y[] = f(v[]), each access stored as soon as it is mapped
+    template <typename F>
+    __device__ __forceinline__ void store(float* y, int N, int tid, F&& f) const {
+        const __amdgpu_buffer_rsrc_t dst = row_rsrc(y, N);
+        const uint32_t o0 = fresh_base_off(tid);
 #pragma unroll
         for (int a = 0; a < NA; ++a) {
-            const int j0 = elem(tid, a, 0);
-            if (j0 < N) {
-                if constexpr (VEC) {
-                    const f32x4_t q = {v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
-                    *reinterpret_cast<f32x4_t*>(y + j0) = q;
-                } else {
-                    y[j0] = v[a];
-                }
-            }
+            Access q;
+            if constexpr (VEC)
+                q = f32x4_t{f(v[4 * a]), f(v[4 * a + 1]), f(v[4 * a + 2]), f(v[4 * a + 3])};
+            else
+                q = f(v[a]);
+            store_at(y, dst, N, o0 + 4u * (uint32_t)first(a), q);
         }
     }
     // f(element index, value) over this thread's elements inside the row
@@ -113,6 +187,43 @@ struct RowRegs {
                 f(j, v[W * a + i], j < N);
             }
     }
+    // The row's tail [nv, N) (N % 16 elements; none when nv == N).  A thread
+    // holds at most one access inside it: the tail has fewer than 16
+    // elements and the group at least 64 threads (with VEC, nv % 16 == 0 and
+    // N % 4 == 0, so a piece is wholly in or out).
+    static constexpr uint32_t TAIL_NONE = 0x80000000u;  // past any row: no store
+    // byte offset of this thread's tail access, or TAIL_NONE: the one element
+    // (piece) u in [nv, N) (pieces [nv/4, N/4)) with u % G == tid
+    __device__ __forceinline__ static uint32_t tail_off(int N, int nv, int tid) {
+        const int u0 = nv / W, u1 = N / W;
+        const int u = u0 + ((tid - u0) & (G - 1));
+        return u < u1 ? (uint32_t)u * (uint32_t)(4 * W) : TAIL_NONE;
+    }
+    // values of that access (0 without one)
+    __device__ __forceinline__ void tail(int N, int nv, int tid, float (&xt)[W]) const {
+#pragma unroll
+        for (int i = 0; i < W; ++i) xt[i] = 0.0f;
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const int j0 = elem(tid, a, 0);
+            const bool t = j0 >= nv && j0 < N;
+#pragma unroll
+            for (int i = 0; i < W; ++i) xt[i] = t ? v[W * a + i] : xt[i];
+        }
+    }
+    // y at byte offset off = q, one float, the same kind of access as store()
+    __device__ __forceinline__ static void store1(float* y, int N, uint32_t off, float q) {
+        RowRegs<G, 1, false>::store_at(y, row_rsrc(y, N), N, off, q);
+    }
+    // this thread's tail access, stored after store() (nothing for TAIL_NONE)
+    __device__ __forceinline__ static void store_tail(float* y, int N, uint32_t toff, const float (&q)[W]) {
+        Access w;
+        if constexpr (VEC)
+            w = f32x4_t{q[0], q[1], q[2], q[3]};
+        else
+            w = q[0];
+        store_at(y, row_rsrc(y, N), N, toff, w);
+    }
 };
 
 // group-wide reductions in a fixed order: a butterfly within each wave, then
@@ -125,7 +236,7 @@ __device__ __forceinline__ float group_max(float v, float* red) {
     } else {
         constexpr int NWV = G / 64;
         __syncthreads();  // red is reused by consecutive reductions
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        if ((threadIdx.x & 63) == 0) red[wave_id()] = v;
         __syncthreads();
         float r[NWV];
 #pragma unroll
@@ -145,7 +256,7 @@ __device__ __forceinline__ float group_sum(float v, float* red) {
     } else {
         constexpr int NWV = G / 64;
         __syncthreads();
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        if ((threadIdx.x & 63) == 0) red[wave_id()] = v;
         __syncthreads();
         float r[NWV];
 #pragma unroll
@@ -158,42 +269,53 @@ __device__ __forceinline__ float group_sum(float v, float* red) {
     }
 }
 
-// softmax of a held row (reference passes: max, exp and sum, scale); returns
-// the sum and leaves p in R.v
+// exponentials and sum of a held row (reference passes: max, exp and sum).
+// Leaves e = fast_exp(x - max) in R.v for the part of the row that fills
+// whole 16-float vectors (j < nv = N & ~15) and 0 elsewhere; the tail
+// [nv, N), where the reference takes expf and divides by the sum instead of
+// multiplying by its reciprocal, is this thread's et[] (its access there:
+// RowRegs::tail_off), to be stored after R.  Each thread sums its own
+// elements, then its tail ones.  FULL: N % 16 == 0, no tail (a kernel of
+// its own, which carries neither the tail's extraction nor its expf).
 template <bool FULL, int G, int ELEMS, bool VEC>
 __device__ __forceinline__ void softmax_held(RowRegs<G, ELEMS, VEC>& R, const float* x, int N,
-                                             int tid, float* red, float* mx_out, float* s_out) {
+                                             int tid, float* red, float* mx_out, float* s_out,
+                                             float (&et)[VEC ? 4 : 1]) {
+    using RR = RowRegs<G, ELEMS, VEC>;
     const int nv = N & ~15;
-    R.load(x, N, tid, -FLT_MAX);
+    R.template load<true>(x, N, tid);
     float mx = -FLT_MAX;
 #pragma unroll
     for (int k = 0; k < ELEMS; ++k) mx = ref_max(mx, R.v[k]);
     mx = group_max<G>(mx, red);
-    float s = 0.0f;
-    // FULL: the row has no tail (N % 16 == 0, the common case), so every
-    // element takes fast_exp and the reciprocal product; a kernel of its own,
-    // which does not carry the registers of the libm tail path
-    if constexpr (FULL) {
-        R.each(N, tid, [&](int, float& e, bool in) {
-            e = in ? fast_exp(e - mx) : 0.0f;
-            s += e;
-        });
-    } else {
-        R.each(N, tid, [&](int j, float& e, bool in) {
-            e = in ? row_exp(e - mx, j, nv) : 0.0f;
-            s += e;
-        });
-    }
-    s = group_sum<G>(s, red);
-    const float inv = 1.0f / s;
     if constexpr (FULL) {
 #pragma unroll
-        for (int k = 0; k < ELEMS; ++k) R.v[k] *= inv;
+        for (int i = 0; i < RR::W; ++i) et[i] = 0.0f;
     } else {
-        R.each(N, tid, [&](int j, float& e, bool) { e = row_norm(e, inv, s, j, nv); });
+        R.tail(N, nv, tid, et);
+    }
+    // fast_exp clamps its argument to [-88, 88], so it is finite for every
+    // element, pads included, and the select needs no branch
+    float s = 0.0f;
+#pragma unroll
+    for (int a = 0; a < RR::NA; ++a)
+#pragma unroll
+        for (int i = 0; i < RR::W; ++i) {
+            float& e = R.v[RR::W * a + i];
+            const float f = fast_exp(e - mx);
+            e = RR::elem(tid, a, i) < nv ? f : 0.0f;
+            s += e;
+        }
+    if constexpr (!FULL) {
+        const bool has_tail = RR::tail_off(N, nv, tid) != RR::TAIL_NONE;
+#pragma unroll
+        for (int i = 0; i < RR::W; ++i) {
+            et[i] = expf(et[i] - mx);
+            s += has_tail ? et[i] : 0.0f;
+        }
     }
     *mx_out = mx;
-    *s_out = s;
+    *s_out = group_sum<G>(s, red);
 }
 
 // row of this block: one per wave (G = 64, ROWS_PER_BLOCK rows) or one per block
@@ -216,9 +338,16 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void softmax_ke
     const int row = held_row<G>(&tid);
     if (row >= M) return;  // whole wave (G = 64) or whole block
     RowRegs<G, ELEMS, VEC> R;
-    float mx, s;
-    softmax_held<FULL>(R, in + (int64_t)row * N, N, tid, red, &mx, &s);
-    R.store(out + (int64_t)row * N, N, tid);
+    float mx, s, pt[VEC ? 4 : 1];
+    softmax_held<FULL>(R, in + (int64_t)row * N, N, tid, red, &mx, &s, pt);
+    const float inv = 1.0f / s;
+    float* y = out + (int64_t)row * N;
+    R.store(y, N, tid, [&](float e) { return e * inv; });
+    if constexpr (!FULL) {
+#pragma unroll
+        for (int i = 0; i < (VEC ? 4 : 1); ++i) pt[i] = pt[i] / s;
+        R.store_tail(y, N, R.tail_off(N, N & ~15, tid), pt);  // after R's store of 0 there
+    }
 }
 
 // ---- rows longer than a block holds: one BT-thread workgroup per row, the
@@ -340,7 +469,7 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void layernorm_
     const int row = held_row<G>(&tid);
     if (row >= M) return;
     RowRegs<G, ELEMS, VEC> R;
-    R.load(in + (int64_t)row * N, N, tid, 0.0f);
+    R.template load<false>(in + (int64_t)row * N, N, tid);
     float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < ELEMS; ++k) s += R.v[k];
@@ -352,22 +481,25 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void layernorm_
     });
     const float var = group_sum<G>(q, red) / (float)N;
     const float inv_std = 1.0f / sqrtf(var + eps);
-    float* y = out + (int64_t)row * N;
     using RR = RowRegs<G, ELEMS, VEC>;
+    float* y = out + (int64_t)row * N;
+    const __amdgpu_buffer_rsrc_t gs = RR::row_rsrc(gamma, N), bs = RR::row_rsrc(beta, N),
+                                 ys = RR::row_rsrc(y, N);
+    const uint32_t o0 = RR::fresh_base_off(tid);
+    const uint32_t last = (uint32_t)(N - RR::W) * 4u;
 #pragma unroll
     for (int a = 0; a < RR::NA; ++a) {
-        const int j0 = RR::elem(tid, a, 0);
-        if (j0 >= N) continue;
+        if (RR::first(a) >= N) continue;  // the same for the whole group
+        const uint32_t o = o0 + 4u * (uint32_t)RR::first(a), oc = o < last ? o : last;
+        const typename RR::Access gq = RR::load_at(gamma, gs, oc), bq = RR::load_at(beta, bs, oc);
+        typename RR::Access q;
         if constexpr (VEC) {
-            const f32x4_t gq = *reinterpret_cast<const f32x4_t*>(gamma + j0);
-            const f32x4_t bq = *reinterpret_cast<const f32x4_t*>(beta + j0);
-            f32x4_t o;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf((R.v[4 * a + i] - mean) * inv_std, gq[i], bq[i]);
-            *reinterpret_cast<f32x4_t*>(y + j0) = o;
+            for (int i = 0; i < 4; ++i) q[i] = __builtin_fmaf((R.v[4 * a + i] - mean) * inv_std, gq[i], bq[i]);
         } else {
-            y[j0] = __builtin_fmaf((R.v[a] - mean) * inv_std, gamma[j0], beta[j0]);
+            q = __builtin_fmaf((R.v[a] - mean) * inv_std, gq, bq);
         }
+        RR::store_at(y, ys, N, o, q);  // nothing past the row
     }
 }
 
@@ -429,30 +561,37 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void cross_entr
     float* g = grad + (int64_t)row * N;
     const int t = targets[row];
     const bool valid = t >= 0 && t < N;
-    // the thread whose elements include t; it reads x[t] before any store of
-    // this row (grad may alias logits)
+    // the thread whose elements include t stores its gradient; x[t] is read
+    // (by every thread, a scalar load) before any store of this row (grad may
+    // alias logits)
     const bool owner = valid && tid == (VEC ? (t >> 2) % G : t % G);
-    const float xt = owner ? x[t] : 0.0f;
+    const float xt = valid ? x[t] : 0.0f;
     RowRegs<G, ELEMS, VEC> R;
-    float mx, s;
-    softmax_held<FULL>(R, x, N, tid, red, &mx, &s);
+    float mx, s, ptl[VEC ? 4 : 1];
+    softmax_held<FULL>(R, x, N, tid, red, &mx, &s, ptl);
     const int nv = N & ~15;
-    const float pt = row_norm(row_exp(xt - mx, t, nv), 1.0f / s, s, t, nv);
+    const float inv = 1.0f / s;
+    const float pt = row_norm(row_exp(xt - mx, t, nv), inv, s, t, nv);
     const float fm = (float)M;
-    // grad / M as the reference's division; for a power-of-two M the product
-    // with 1/M (exact) is the same single rounding of x * 2^-k, bit for bit,
-    // at a tenth of the instructions
+#pragma unroll
+    for (int i = 0; i < (VEC ? 4 : 1); ++i) ptl[i] = ptl[i] / s;
+    // grad = p / M as the reference's division; for a power-of-two M the
+    // product with 1/M (exact) is the same single rounding of p * 2^-k, bit
+    // for bit, at a tenth of the instructions
     if ((M & (M - 1)) == 0) {
         const float rm = 1.0f / fm;
+        R.store(g, N, tid, [&](float e) { return (e * inv) * rm; });
 #pragma unroll
-        for (int k = 0; k < ELEMS; ++k) R.v[k] = R.v[k] * rm;
+        for (int i = 0; i < (VEC ? 4 : 1); ++i) ptl[i] = ptl[i] * rm;
     } else {
+        R.store(g, N, tid, [&](float e) { return (e * inv) / fm; });
 #pragma unroll
-        for (int k = 0; k < ELEMS; ++k) R.v[k] = R.v[k] / fm;
+        for (int i = 0; i < (VEC ? 4 : 1); ++i) ptl[i] = ptl[i] / fm;
     }
-    R.store(g, N, tid);
+    if constexpr (!FULL) R.store_tail(g, N, R.tail_off(N, nv, tid), ptl);  // after R's store of 0 there
     if (owner) {
-        g[t] = (pt - 1.0f) / fm;  // after this thread's own store of g[t]
+        // after this thread's own stores of g[t], through the same buffer path
+        R.store1(g, N, (uint32_t)t * 4u, (pt - 1.0f) / fm);
         row_loss[row] = -logf(pt + 1e-10f);
     } else if (!valid && tid == 0) {
         row_loss[row] = __builtin_nanf("");
@@ -563,10 +702,11 @@ hipError_t by_size(int N, bool vec, F&& f) {
     if (N <= 512) return with_flags<64, 8>(vec, full, f);
     if (N <= 1024) return with_flags<64, 16>(vec, full, f);
     if (N <= 2048) return with_flags<64, 32>(vec, full, f);
-    if (N <= 4096) return with_flags<64, 64>(vec, full, f);
+    if (N <= MAX_CACHED) return with_flags<64, 64>(vec, full, f);
     if (N <= 8192) return with_flags<BT, 8>(vec, full, f);
     if (N <= 16384) return with_flags<BT, 16>(vec, full, f);
-    return with_flags<BT, 32>(vec, full, f);
+    if (N <= 32768) return with_flags<BT, 32>(vec, full, f);
+    return with_flags<BT, MAX_BLOCK_CACHED / BT>(vec, full, f);
 }
 
 bool rows_vec4(int N, std::initializer_list<const void*> ptrs) {

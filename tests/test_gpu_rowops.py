@@ -8,10 +8,10 @@ order instead of the reference's 16 lane partials).  Shapes cover the
 reference's own benchmark shapes (softmax [64,256], [64,10], [2048,2048];
 layernorm [64,256], [2048,256]), the 16-element vector/tail split (N = 15,
 16, 17, 33), N = 1, ragged M, rows held in registers at every cache size,
-rows of 4097-32768 held by one 1024-thread block (16-byte and 4-byte
-accesses), rows longer than 32768 (the streaming passes, 16-byte and 4-byte
-accesses, up to 131073), rows that are not 16-byte aligned (the 4-byte path)
-and in-place softmax and cross entropy, held and streamed."""
+rows of 4097-65536 held by one 1024-thread block (16-byte and 4-byte
+accesses, with and without a tail), rows longer than 65536 (the streaming
+passes, 16-byte and 4-byte accesses, up to 131073), rows that are not
+16-byte aligned (the 4-byte path) and in-place softmax and cross entropy."""
 import numpy as np
 import pytest
 import torch
@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 SHAPES = [(64, 256), (64, 10), (2048, 2048), (2048, 256), (1, 1), (3, 15), (5, 16), (7, 17),
           (9, 33), (13, 100), (6, 600), (5, 1500), (3, 4000), (3, 4096), (2, 4097), (2, 10000),
           (3, 16386), (2, 20001), (2, 32768), (2, 32769), (2, 40000), (2, 50257), (2, 65536),
-          (1, 131073)]
+          (2, 65537), (1, 131073)]
 
 
 def _x(M, N, seed, scale=3.0):
@@ -92,7 +92,7 @@ def test_softmax(dev, M, N):
     assert np.abs(y.astype(np.float64).sum(1) - 1.0).max() < 1e-5
 
 
-@pytest.mark.parametrize("N", [300, 40000])
+@pytest.mark.parametrize("N", [300, 40000, 70001])
 def test_softmax_in_place_and_extremes(dev, N):
     case(f"softmax in place, large and -inf logits N={N}")
     x = _x(16, N, 5, scale=40.0)
@@ -138,7 +138,7 @@ def test_layernorm_epsilon_and_constant_rows(dev):
 
 @pytest.mark.parametrize("M,N", [(64, 10), (128, 1000), (7, 17), (1, 1), (5, 4096), (3, 7000),
                                  (2048, 512), (3, 32000), (2, 20001), (2, 40000), (2, 50257),
-                                 (2, 131072)])
+                                 (2, 65537), (2, 131072)])
 def test_cross_entropy(dev, M, N):
     case(f"cross entropy [{M},{N}]")
     x = _x(M, N, 3 * M + N)
@@ -191,7 +191,7 @@ def test_cross_entropy_bad_target_and_repeat(dev):
     np.testing.assert_allclose(to_np(g2)[2], po.softmax(x)[2] / 6, rtol=2e-6)
 
 
-@pytest.mark.parametrize("N", [256, 2048, 8192, 40000])
+@pytest.mark.parametrize("N", [256, 2048, 8192, 40000, 70000])
 def test_unaligned_rows_and_in_place(dev, N):
     """Rows whose start is only 4-byte aligned take the 4-byte path (same
     results); cross entropy with grad written over the logits."""
