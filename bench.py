@@ -10,7 +10,7 @@ synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 The same run also times every BASELINE config on its own (per_config, keys
 c1-c5; c5p is C5 on the packed weight layout), the reference's published shapes (per_config, keys
 g1-g3: fp32 matmuls, a1: fp32 non-causal flash attention; each beside its published time and the
-ratio to it), the row kernels (per_config, keys r1-r6: softmax, layernorm, cross
+ratio to it), the row kernels (per_config, keys r1-r8: softmax, layernorm, cross
 entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
 (per_config, keys m1-m2, fp32 TFLOP/s), the flash-attention backward at C4's
 shape (per_config, key b4), matmulInt8 (per_config, keys i1-i2: int8 TOP/s at
@@ -75,7 +75,10 @@ PACKED_CONFIGS = {
 
 # Row kernels (the next rows of the hot-path scope; not BASELINE configs):
 # the reference's own benchmark shapes (bench_kernel.cpp:396-399, :450-453)
-# and one large shape each, where launch latency does not dominate.
+# and one large shape each, where launch latency does not dominate; then the
+# cross entropy of a language-model head at two vocabulary sizes: 50257 (a
+# row held at 64 elements per thread, 4-byte accesses, a tail) and 128256
+# (rows streamed in three passes).
 ROW_CONFIGS = {
     "r1": dict(kind="softmax", M=2048, N=2048),
     "r2": dict(kind="softmax", M=16384, N=4096),
@@ -83,6 +86,8 @@ ROW_CONFIGS = {
     "r4": dict(kind="layernorm", M=16384, N=4096),
     "r5": dict(kind="xent", M=16384, N=4096),
     "r6": dict(kind="xent", M=4096, N=32000),
+    "r7": dict(kind="xent", M=2048, N=50257),
+    "r8": dict(kind="xent", M=512, N=128256),
 }
 
 
