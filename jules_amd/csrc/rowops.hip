@@ -19,11 +19,11 @@
 // elements per thread).  With N % 4 == 0 and 16-byte aligned rows each
 // thread moves 16-byte pieces, otherwise single floats; either way every wave
 // instruction covers contiguous bytes.  Rows longer than 65536 get a
-// 1024-thread workgroup that streams the row three times in chunks of 16
-// elements per thread, in the reference's own passes (softmax and cross
-// entropy: max, sum of exponentials, write with the exponentials recomputed;
-// layernorm: sum, squared deviations, write); the later passes mostly find
-// the row in the caches.  Reductions are a fixed butterfly within a wave and
+// 1024-thread workgroup that keeps the row's first 65536 elements on chip
+// (registers and LDS) and streams the rest in chunks of 16 elements per
+// thread, in the reference's own three passes (softmax and cross entropy:
+// max, sum of exponentials, write with the exponentials recomputed;
+// layernorm: sum, squared deviations, write).  Reductions are a fixed butterfly within a wave and
 // a fixed tree across waves, so results are deterministic.
 #include <cfloat>
 #include <type_traits>
@@ -410,20 +410,104 @@ struct Chunk {
     }
 };
 
-// f(chunk start b, elements left rem) over the chunks of a row of N
+// f(chunk start b, elements left rem) over the chunks of a row of N from b0
 template <typename F>
-__device__ __forceinline__ void chunks(int N, F&& f) {
-    for (int64_t b = 0; b < N; b += LCH) f((int)b, (int)(N - b));
+__device__ __forceinline__ void chunks(int b0, int N, F&& f) {
+    for (int64_t b = b0; b < N; b += LCH) f((int)b, (int)(N - b));
 }
 
-// row max, then the sum of exp(x - max) (reference passes 1a and 1b), each
-// streaming the row
+// The head of a long row, its first HEAD_CHUNKS chunks (65536 elements;
+// every long row has all of them whole), stays on chip after the first read:
+// chunks 0 and 1 in registers, chunks 2 and 3 in this thread's part of a
+// dynamic LDS area (element k of chunk 2 + h at area[(h * LE + k) * BT +
+// tid]: consecutive threads in consecutive banks, and no thread reads
+// another's slots, so no barrier).  The later passes re-read only the rest
+// of the row.  Every pass visits the head's elements in chunk order, each
+// chunk in the order of Chunk::each, so sums are taken in the same order as
+// over a streamed row.
+constexpr int HEAD_CHUNKS = 4;
+constexpr size_t HEAD_LDS = 2 * LE * BT * sizeof(float);  // 128 KiB
+static_assert(HEAD_CHUNKS * LCH == MAX_BLOCK_CACHED, "long rows hold the whole head");
+
 template <bool VEC>
-__device__ __forceinline__ void long_row_stats(const float* x, int N, float* red, float* mx_out,
-                                               float* s_out) {
+struct Head {
+    using C = Chunk<VEC>;
+    C r[2];
+    float* area;
+    __device__ __forceinline__ explicit Head(float* lds) : area(lds + threadIdx.x) {}
+    __device__ __forceinline__ float& slot(int h, int k) { return area[(h * LE + k) * BT]; }
+    // offset in its chunk of this thread's element k
+    __device__ __forceinline__ static int off(int k) { return C::off(k / C::W, k % C::W); }
+    // loads the head, f(element index, value) over it in order
+    template <typename F>
+    __device__ __forceinline__ void load(const float* x, F&& f) {
+        C c2, c3;
+        r[0].load(x, LCH, 0.0f);
+        r[1].load(x + LCH, LCH, 0.0f);
+        c2.load(x + 2 * LCH, LCH, 0.0f);
+        c3.load(x + 3 * LCH, LCH, 0.0f);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int k = 0; k < LE; ++k) f(h * LCH + off(k), r[h].v[k]);
+#pragma unroll
+        for (int k = 0; k < LE; ++k) {
+            f(2 * LCH + off(k), c2.v[k]);
+            slot(0, k) = c2.v[k];
+        }
+#pragma unroll
+        for (int k = 0; k < LE; ++k) {
+            f(3 * LCH + off(k), c3.v[k]);
+            slot(1, k) = c3.v[k];
+        }
+    }
+    // f(element index, value&) over the head in order; with WB the LDS
+    // values are written back
+    template <bool WB, typename F>
+    __device__ __forceinline__ void each(F&& f) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int k = 0; k < LE; ++k) f(h * LCH + off(k), r[h].v[k]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int k = 0; k < LE; ++k) {
+                float v = slot(h, k);
+                f((2 + h) * LCH + off(k), v);
+                if constexpr (WB) slot(h, k) = v;
+            }
+    }
+    // y = the head mapped chunk by chunk: f(chunk start, chunk) rewrites the
+    // chunk's values, which are then stored
+    template <typename F>
+    __device__ __forceinline__ void map_store(float* y, F&& f) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f(h * LCH, r[h]);
+            r[h].store(y + h * LCH, LCH);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            C c;
+#pragma unroll
+            for (int k = 0; k < LE; ++k) c.v[k] = slot(h, k);
+            f((2 + h) * LCH, c);
+            c.store(y + (2 + h) * LCH, LCH);
+        }
+    }
+};
+
+// row max, then the sum of exp(x - max) (reference passes 1a and 1b); the
+// head's exponentials are left in H (all of the head is in the vector part)
+template <bool VEC>
+__device__ __forceinline__ void long_row_stats(Head<VEC>& H, const float* x, int N, float* red,
+                                               float* mx_out, float* s_out) {
+    constexpr int B0 = HEAD_CHUNKS * LCH;
     const int nv = N & ~15;
     float mx = -FLT_MAX;
-    chunks(N, [&](int b, int rem) {
+    H.load(x, [&](int, float v) { mx = ref_max(mx, v); });
+    chunks(B0, N, [&](int b, int rem) {
         Chunk<VEC> C;
         C.load(x + b, rem, -FLT_MAX);
 #pragma unroll
@@ -431,7 +515,11 @@ __device__ __forceinline__ void long_row_stats(const float* x, int N, float* red
     });
     mx = group_max<BT>(mx, red);
     float s = 0.0f;
-    chunks(N, [&](int b, int rem) {
+    H.template each<true>([&](int, float& e) {
+        e = fast_exp(e - mx);
+        s += e;
+    });
+    chunks(B0, N, [&](int b, int rem) {
         Chunk<VEC> C;
         C.load(x + b, rem, 0.0f);
         C.each(rem, [&](int o, float e, bool in) { s += in ? row_exp(e - mx, b + o, nv) : 0.0f; });
@@ -443,13 +531,19 @@ __device__ __forceinline__ void long_row_stats(const float* x, int N, float* red
 template <bool VEC>
 __global__ __launch_bounds__(BT) void softmax_long_kernel(float* out, const float* in, int N) {
     __shared__ float red[BT / 64];
+    extern __shared__ float head_lds[];
     const float* x = in + (int64_t)blockIdx.x * N;
     float* y = out + (int64_t)blockIdx.x * N;
     const int nv = N & ~15;
+    Head<VEC> H(head_lds);
     float mx, s;
-    long_row_stats<VEC>(x, N, red, &mx, &s);
+    long_row_stats<VEC>(H, x, N, red, &mx, &s);
     const float inv = 1.0f / s;
-    chunks(N, [&](int b, int rem) {
+    H.map_store(y, [&](int, Chunk<VEC>& c) {
+#pragma unroll
+        for (int k = 0; k < LE; ++k) c.v[k] *= inv;
+    });
+    chunks(HEAD_CHUNKS * LCH, N, [&](int b, int rem) {
         Chunk<VEC> C;
         C.load(x + b, rem, 0.0f);
         C.each(rem, [&](int o, float& e, bool) {
@@ -504,17 +598,21 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void layernorm_
 }
 
 // rows longer than a block holds: the reference's three passes (sum, sum of
-// squared deviations, write), each streaming the row in chunks
+// squared deviations, write), the head held on chip and the rest streamed
 template <bool VEC>
 __global__ __launch_bounds__(BT) void layernorm_long_kernel(float* out, const float* in,
                                                            const float* __restrict__ gamma,
                                                            const float* __restrict__ beta, int N,
                                                            float eps) {
+    constexpr int B0 = HEAD_CHUNKS * LCH;
     __shared__ float red[BT / 64];
+    extern __shared__ float head_lds[];
     const float* x = in + (int64_t)blockIdx.x * N;
     float* y = out + (int64_t)blockIdx.x * N;
+    Head<VEC> H(head_lds);
     float s = 0.0f;
-    chunks(N, [&](int b, int rem) {
+    H.load(x, [&](int, float v) { s += v; });
+    chunks(B0, N, [&](int b, int rem) {
         Chunk<VEC> C;
         C.load(x + b, rem, 0.0f);
 #pragma unroll
@@ -522,7 +620,11 @@ __global__ __launch_bounds__(BT) void layernorm_long_kernel(float* out, const fl
     });
     const float mean = group_sum<BT>(s, red) / (float)N;
     float q = 0.0f;
-    chunks(N, [&](int b, int rem) {
+    H.template each<false>([&](int, float& v) {
+        const float d = v - mean;
+        q = __builtin_fmaf(d, d, q);
+    });
+    chunks(B0, N, [&](int b, int rem) {
         Chunk<VEC> C;
         C.load(x + b, rem, 0.0f);
         C.each(rem, [&](int, float e, bool in) {
@@ -532,13 +634,18 @@ __global__ __launch_bounds__(BT) void layernorm_long_kernel(float* out, const fl
     });
     const float var = group_sum<BT>(q, red) / (float)N;
     const float inv_std = 1.0f / sqrtf(var + eps);
-    chunks(N, [&](int b, int rem) {
-        Chunk<VEC> C, G, B;
-        C.load(x + b, rem, 0.0f);
+    auto write = [&](int b, int rem, Chunk<VEC>& C) {
+        Chunk<VEC> G, B;
         G.load(gamma + b, rem, 0.0f);
         B.load(beta + b, rem, 0.0f);
 #pragma unroll
         for (int k = 0; k < LE; ++k) C.v[k] = __builtin_fmaf((C.v[k] - mean) * inv_std, G.v[k], B.v[k]);
+    };
+    H.map_store(y, [&](int b, Chunk<VEC>& c) { write(b, LCH, c); });
+    chunks(B0, N, [&](int b, int rem) {
+        Chunk<VEC> C;
+        C.load(x + b, rem, 0.0f);
+        write(b, rem, C);
         C.store(y + b, rem);
     });
 }
@@ -603,21 +710,27 @@ __global__ __launch_bounds__(BT) void cross_entropy_long_kernel(const float* log
                                                                const int32_t* targets, float* grad,
                                                                float* row_loss, int M, int N) {
     __shared__ float red[BT / 64];
+    extern __shared__ float head_lds[];
     const int row = blockIdx.x;
     const float* x = logits + (int64_t)row * N;
     float* g = grad + (int64_t)row * N;
     const int nv = N & ~15;
-    float mx, s;
     const int t = targets[row];
     const bool valid = t >= 0 && t < N;
     const bool owner = valid && (int)threadIdx.x == (VEC ? t >> 2 : t) % BT;  // Chunk's owner of t
-    const float xt = owner ? x[t] : 0.0f;  // before any store of this row (grad may alias logits)
-    long_row_stats<VEC>(x, N, red, &mx, &s);
+    const float xt = valid ? x[t] : 0.0f;  // before any store of this row (grad may alias logits)
+    Head<VEC> H(head_lds);
+    float mx, s;
+    long_row_stats<VEC>(H, x, N, red, &mx, &s);
     const float inv = 1.0f / s;
     const float fm = (float)M;
     const bool pow2 = (M & (M - 1)) == 0;  // exact product with 1/M, as in cross_entropy_kernel
     const float rm = 1.0f / fm;
-    chunks(N, [&](int b, int rem) {
+    H.map_store(g, [&](int, Chunk<VEC>& c) {
+#pragma unroll
+        for (int k = 0; k < LE; ++k) c.v[k] = pow2 ? (c.v[k] * inv) * rm : (c.v[k] * inv) / fm;
+    });
+    chunks(HEAD_CHUNKS * LCH, N, [&](int b, int rem) {
         Chunk<VEC> C;
         C.load(x + b, rem, 0.0f);
         C.each(rem, [&](int o, float& e, bool) {
@@ -727,9 +840,9 @@ hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t
     if (M == 0) return hipSuccess;
     if (N > MAX_BLOCK_CACHED) {
         if (rows_vec4(N, {out, in}))
-            hipLaunchKernelGGL(softmax_long_kernel<true>, dim3(M), dim3(BT), 0, s, out, in, N);
+            hipLaunchKernelGGL(softmax_long_kernel<true>, dim3(M), dim3(BT), HEAD_LDS, s, out, in, N);
         else
-            hipLaunchKernelGGL(softmax_long_kernel<false>, dim3(M), dim3(BT), 0, s, out, in, N);
+            hipLaunchKernelGGL(softmax_long_kernel<false>, dim3(M), dim3(BT), HEAD_LDS, s, out, in, N);
         return hipGetLastError();
     }
     return by_size(N, rows_vec4(N, {out, in}), [&](auto g, auto e, auto v, auto f) {
@@ -746,10 +859,10 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
     if (M == 0) return hipSuccess;
     if (N > MAX_BLOCK_CACHED) {
         if (rows_vec4(N, {out, in, gamma, beta}))
-            hipLaunchKernelGGL(layernorm_long_kernel<true>, dim3(M), dim3(BT), 0, s, out, in, gamma,
+            hipLaunchKernelGGL(layernorm_long_kernel<true>, dim3(M), dim3(BT), HEAD_LDS, s, out, in, gamma,
                                beta, N, eps);
         else
-            hipLaunchKernelGGL(layernorm_long_kernel<false>, dim3(M), dim3(BT), 0, s, out, in, gamma,
+            hipLaunchKernelGGL(layernorm_long_kernel<false>, dim3(M), dim3(BT), HEAD_LDS, s, out, in, gamma,
                                beta, N, eps);
         return hipGetLastError();
     }
@@ -768,10 +881,10 @@ hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, flo
     if (M > 0) {
         if (N > MAX_BLOCK_CACHED) {
             if (rows_vec4(N, {logits, grad}))
-                hipLaunchKernelGGL(cross_entropy_long_kernel<true>, dim3(M), dim3(BT), 0, s, logits,
+                hipLaunchKernelGGL(cross_entropy_long_kernel<true>, dim3(M), dim3(BT), HEAD_LDS, s, logits,
                                    targets, grad, row_loss, M, N);
             else
-                hipLaunchKernelGGL(cross_entropy_long_kernel<false>, dim3(M), dim3(BT), 0, s, logits,
+                hipLaunchKernelGGL(cross_entropy_long_kernel<false>, dim3(M), dim3(BT), HEAD_LDS, s, logits,
                                    targets, grad, row_loss, M, N);
             e = hipGetLastError();
         } else {
