@@ -281,6 +281,8 @@ int jules_hip_w8a16_noalloc_counters(uint32_t* out, int n);
  * (The reference's AVX-512F and VNNI paths index the wrong columns; this
  * entry point follows the scalar path.)  K <= 131071 keeps the int32 sum
  * exact (every product is at most 2^14); larger K returns JH_ERR_SHAPE.
+ * M <= 16 (decode) keeps its split-K partials in a device buffer the library
+ * keeps per (device, stream), allocated on the first call that needs it.
  */
 int jules_hip_matmul_int8(const int8_t* A, const int8_t* B, float* C, int M,
                           int N, int K, float scale_A, float scale_B,
@@ -307,6 +309,10 @@ int jules_hip_matmul_w8a8(const int8_t* A, const int8_t* B, float* C, int M,
  * split: fast_exp for j < N & ~15, expf for the tail; reciprocal multiply
  * vs divide likewise); sums are taken in a fixed tree order, so results
  * match the reference to rounding and are deterministic run to run.
+ * Up to 64 rows longer than 65536 are split over workgroups (three
+ * launches); their partial maxima and sums, 8*M*ceil(N/4096) bytes, go to a
+ * device buffer the library keeps per (device, stream), allocated on the
+ * first call that needs it (calls on one stream share it in order).
  *
  * jules_hip_softmax: out[i,:] = softmax(in[i,:]).
  *   Replaces fusedSoftmax(output, input, M, N)

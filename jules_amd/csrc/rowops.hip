@@ -356,16 +356,16 @@ __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void softmax_ke
 constexpr int LE = 16;          // elements per thread per chunk (its loads in flight)
 constexpr int LCH = BT * LE;    // elements per chunk
 
-template <bool VEC>
+template <bool VEC, int T = BT>
 struct Chunk {
     static constexpr int W = VEC ? 4 : 1;
     static constexpr int NA = LE / W;
     float v[LE];
-    // offset in the chunk of this thread's access a, element i; a chunk
-    // starts at a multiple of LCH, so element j of the row belongs to thread
-    // (VEC ? j / 4 : j) % BT
+    // offset in the chunk of this thread's access a, element i (T threads,
+    // T * LE elements); a chunk starts at a multiple of T * LE, so element j
+    // of the row belongs to thread (VEC ? j / 4 : j) % T
     __device__ __forceinline__ static int off(int a, int i) {
-        return VEC ? 4 * ((int)threadIdx.x + BT * a) + i : (int)threadIdx.x + BT * a;
+        return VEC ? 4 * ((int)threadIdx.x + T * a) + i : (int)threadIdx.x + T * a;
     }
     // v[] = x[0 .. rem) of the chunk starting at x, pad past it (rem > 0;
     // with VEC rem % 4 == 0)
@@ -748,6 +748,160 @@ __global__ __launch_bounds__(BT) void cross_entropy_long_kernel(const float* log
     }
 }
 
+// ---- few long rows: each row split into segments of SEG elements, one
+// ST-thread workgroup per segment, in three launches (the reference's three
+// passes), so that M rows fill M * ceil(N / SEG) workgroups instead of M.
+// Launch 1 writes each segment's max (layernorm: its sum) to part1; launch 2
+// reduces the row's part1 to the row max (mean) and writes each segment's
+// sum of exponentials (squared deviations) to part2; launch 3 reduces both
+// and writes the segment.  Every workgroup of a row reduces the row's
+// partials with the same code in the same order, so all of them hold the
+// same max and sum; results are deterministic (a row sum is taken within
+// each segment, then over the segments in a fixed order).  The per-element
+// arithmetic is the reference's, as in the other row kernels. ----
+constexpr int ST = 256;       // threads per segment workgroup
+constexpr int SEG = ST * LE;  // elements per segment
+
+struct SegPos {
+    int row, b, rem;  // row, segment start, elements from there to the row's end
+};
+__device__ __forceinline__ SegPos seg_pos(int N, int nseg) {
+    SegPos p;
+    p.row = (int)blockIdx.x / nseg;
+    p.b = ((int)blockIdx.x - p.row * nseg) * SEG;
+    p.rem = N - p.b;
+    return p;
+}
+// a row's nseg partials reduced in a fixed order (thread i takes i, i + ST, ...)
+__device__ __forceinline__ float parts_max(const float* part, int nseg, float* red) {
+    float m = -FLT_MAX;
+    for (int i = threadIdx.x; i < nseg; i += ST) m = ref_max(m, part[i]);
+    return group_max<ST>(m, red);
+}
+__device__ __forceinline__ float parts_sum(const float* part, int nseg, float* red) {
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < nseg; i += ST) s += part[i];
+    return group_sum<ST>(s, red);
+}
+
+// launch 1: segment max (softmax, cross entropy) or sum (layernorm)
+template <bool VEC, bool SUM>
+__global__ __launch_bounds__(ST) void seg_pass1_kernel(const float* in, int N, int nseg,
+                                                       float* __restrict__ part1) {
+    __shared__ float red[ST / 64];
+    const SegPos p = seg_pos(N, nseg);
+    Chunk<VEC, ST> C;
+    C.load(in + (int64_t)p.row * N + p.b, p.rem, SUM ? 0.0f : -FLT_MAX);
+    float v = SUM ? 0.0f : -FLT_MAX;
+#pragma unroll
+    for (int k = 0; k < LE; ++k) v = SUM ? v + C.v[k] : ref_max(v, C.v[k]);
+    v = SUM ? group_sum<ST>(v, red) : group_max<ST>(v, red);
+    if (threadIdx.x == 0) part1[blockIdx.x] = v;
+}
+
+// launch 2: the segment's sum of exponentials at the row max (SUM = false) or
+// of squared deviations from the row mean (SUM = true, layernorm)
+template <bool VEC, bool SUM>
+__global__ __launch_bounds__(ST) void seg_pass2_kernel(const float* in, int N, int nseg,
+                                                       const float* __restrict__ part1,
+                                                       float* __restrict__ part2) {
+    __shared__ float red[ST / 64];
+    const SegPos p = seg_pos(N, nseg);
+    const int nv = N & ~15;
+    Chunk<VEC, ST> C;
+    C.load(in + (int64_t)p.row * N + p.b, p.rem, 0.0f);
+    const float* pr = part1 + (int64_t)p.row * nseg;
+    const float ref = SUM ? parts_sum(pr, nseg, red) / (float)N : parts_max(pr, nseg, red);
+    float s = 0.0f;
+    C.each(p.rem, [&](int o, float e, bool in) {
+        if constexpr (SUM) {
+            const float d = e - ref;
+            s = in ? __builtin_fmaf(d, d, s) : s;
+        } else {
+            s += in ? row_exp(e - ref, p.b + o, nv) : 0.0f;
+        }
+    });
+    s = group_sum<ST>(s, red);
+    if (threadIdx.x == 0) part2[blockIdx.x] = s;
+}
+
+// launch 3, softmax
+template <bool VEC>
+__global__ __launch_bounds__(ST) void softmax_seg_write_kernel(float* out, const float* in, int N,
+                                                               int nseg, const float* __restrict__ part1,
+                                                               const float* __restrict__ part2) {
+    __shared__ float red[ST / 64];
+    const SegPos p = seg_pos(N, nseg);
+    const int nv = N & ~15;
+    Chunk<VEC, ST> C;
+    C.load(in + (int64_t)p.row * N + p.b, p.rem, 0.0f);
+    const float mx = parts_max(part1 + (int64_t)p.row * nseg, nseg, red);
+    const float s = parts_sum(part2 + (int64_t)p.row * nseg, nseg, red);
+    const float inv = 1.0f / s;
+    C.each(p.rem, [&](int o, float& e, bool) {
+        e = row_norm(row_exp(e - mx, p.b + o, nv), inv, s, p.b + o, nv);
+    });
+    C.store(out + (int64_t)p.row * N + p.b, p.rem);
+}
+
+// launch 3, layernorm
+template <bool VEC>
+__global__ __launch_bounds__(ST) void layernorm_seg_write_kernel(
+    float* out, const float* in, const float* __restrict__ gamma, const float* __restrict__ beta,
+    int N, float eps, int nseg, const float* __restrict__ part1, const float* __restrict__ part2) {
+    __shared__ float red[ST / 64];
+    const SegPos p = seg_pos(N, nseg);
+    Chunk<VEC, ST> C, G, B;
+    C.load(in + (int64_t)p.row * N + p.b, p.rem, 0.0f);
+    G.load(gamma + p.b, p.rem, 0.0f);
+    B.load(beta + p.b, p.rem, 0.0f);
+    const float mean = parts_sum(part1 + (int64_t)p.row * nseg, nseg, red) / (float)N;
+    const float var = parts_sum(part2 + (int64_t)p.row * nseg, nseg, red) / (float)N;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int k = 0; k < LE; ++k) C.v[k] = __builtin_fmaf((C.v[k] - mean) * inv_std, G.v[k], B.v[k]);
+    C.store(out + (int64_t)p.row * N + p.b, p.rem);
+}
+
+// launch 3, cross entropy: the segment's gradient; the workgroup whose
+// segment holds the target also writes the row loss
+template <bool VEC>
+__global__ __launch_bounds__(ST) void cross_entropy_seg_write_kernel(
+    const float* logits, const int32_t* targets, float* grad, float* row_loss, int M, int N,
+    int nseg, const float* __restrict__ part1, const float* __restrict__ part2) {
+    __shared__ float red[ST / 64];
+    const SegPos p = seg_pos(N, nseg);
+    const int nv = N & ~15;
+    const float* x = logits + (int64_t)p.row * N;
+    float* g = grad + (int64_t)p.row * N;
+    const int t = targets[p.row];
+    const bool valid = t >= 0 && t < N;
+    const bool mine = valid && t >= p.b && t < p.b + SEG;  // the target is in this segment
+    // the thread whose element t is (Chunk's layout from the segment start)
+    const bool owner = mine && (int)threadIdx.x == (VEC ? (t - p.b) >> 2 : t - p.b) % ST;
+    Chunk<VEC, ST> C;
+    C.load(x + p.b, p.rem, 0.0f);
+    const float xt = mine ? x[t] : 0.0f;  // before this workgroup's stores (grad may alias logits)
+    const float mx = parts_max(part1 + (int64_t)p.row * nseg, nseg, red);
+    const float s = parts_sum(part2 + (int64_t)p.row * nseg, nseg, red);
+    const float inv = 1.0f / s;
+    const float fm = (float)M;
+    const bool pow2 = (M & (M - 1)) == 0;  // exact product with 1/M, as in cross_entropy_kernel
+    const float rm = 1.0f / fm;
+    C.each(p.rem, [&](int o, float& e, bool) {
+        const float pv = row_norm(row_exp(e - mx, p.b + o, nv), inv, s, p.b + o, nv);
+        e = pow2 ? pv * rm : pv / fm;
+    });
+    C.store(g + p.b, p.rem);
+    if (owner) {
+        const float pt = row_norm(row_exp(xt - mx, t, nv), inv, s, t, nv);
+        g[t] = (pt - 1.0f) / fm;  // after this thread's own store of g[t]
+        row_loss[p.row] = -logf(pt + 1e-10f);
+    } else if (!valid && p.b == 0 && threadIdx.x == 0) {
+        row_loss[p.row] = __builtin_nanf("");
+    }
+}
+
 // loss = sum of row_loss in a fixed order / M (one workgroup of RT threads).
 // Thread i adds rows i, i + RT, i + 2 RT, ..., RU of them per round with all
 // RU loads in flight together (a loop of dependent load-add steps waited out
@@ -834,10 +988,64 @@ unsigned row_blocks(int M) {
     return G == 64 ? (unsigned)((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK) : (unsigned)M;
 }
 
+// Few long rows: each row split over workgroups (three launches) when one
+// workgroup per row would leave most CUs idle streaming it.  Measured: the
+// three launches cost ~10 us together, so rows the block-held kernels take
+// (N <= 65536) stay there (8 x 8192: 4.0 vs 10.8 us; 16 x 32000: 7.2 vs
+// 11.4 us), while longer rows gain (1 x 128256: 30.2 -> 11.2 us; 64 x 128256:
+// 34.6 -> 25.1 us) up to 64 rows (128 x 128256: 43.3 vs 46.3 us).
+constexpr int SPLIT_MAX_ROWS = 64;
+bool split_rows(int M, int N) { return M <= SPLIT_MAX_ROWS && N > MAX_BLOCK_CACHED; }
+
+// launches 1 and 2 of a split row op; write(vec, grid, part1, part2) issues
+// launch 3.  The partials (2 M ceil(N / SEG) floats) live in the stream's
+// workspace.
+template <typename W>
+hipError_t launch_split(int M, int N, bool vec, bool layer, const float* x, hipStream_t s, W&& write) {
+    const int nseg = (N + SEG - 1) / SEG;
+    void* ws = nullptr;
+    hipError_t e = stream_workspace(2 * (size_t)M * (size_t)nseg * sizeof(float), s, &ws);
+    if (e != hipSuccess) return e;
+    float* part1 = static_cast<float*>(ws);
+    float* part2 = part1 + (size_t)M * (size_t)nseg;
+    const dim3 grid((unsigned)(M * nseg)), blk(ST);
+    if (vec) {
+        if (layer) {
+            hipLaunchKernelGGL((seg_pass1_kernel<true, true>), grid, blk, 0, s, x, N, nseg, part1);
+            hipLaunchKernelGGL((seg_pass2_kernel<true, true>), grid, blk, 0, s, x, N, nseg, part1, part2);
+        } else {
+            hipLaunchKernelGGL((seg_pass1_kernel<true, false>), grid, blk, 0, s, x, N, nseg, part1);
+            hipLaunchKernelGGL((seg_pass2_kernel<true, false>), grid, blk, 0, s, x, N, nseg, part1, part2);
+        }
+    } else {
+        if (layer) {
+            hipLaunchKernelGGL((seg_pass1_kernel<false, true>), grid, blk, 0, s, x, N, nseg, part1);
+            hipLaunchKernelGGL((seg_pass2_kernel<false, true>), grid, blk, 0, s, x, N, nseg, part1, part2);
+        } else {
+            hipLaunchKernelGGL((seg_pass1_kernel<false, false>), grid, blk, 0, s, x, N, nseg, part1);
+            hipLaunchKernelGGL((seg_pass2_kernel<false, false>), grid, blk, 0, s, x, N, nseg, part1, part2);
+        }
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    write(vec, grid, nseg, part1, part2);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t s) {
     if (M == 0) return hipSuccess;
+    if (split_rows(M, N)) {
+        return launch_split(M, N, rows_vec4(N, {out, in}), false, in, s,
+                            [&](bool vec, dim3 grid, int nseg, const float* p1, const float* p2) {
+                                if (vec)
+                                    hipLaunchKernelGGL(softmax_seg_write_kernel<true>, grid, dim3(ST), 0, s,
+                                                       out, in, N, nseg, p1, p2);
+                                else
+                                    hipLaunchKernelGGL(softmax_seg_write_kernel<false>, grid, dim3(ST), 0, s,
+                                                       out, in, N, nseg, p1, p2);
+                            });
+    }
     if (N > MAX_BLOCK_CACHED) {
         if (rows_vec4(N, {out, in}))
             hipLaunchKernelGGL(softmax_long_kernel<true>, dim3(M), dim3(BT), HEAD_LDS, s, out, in, N);
@@ -857,6 +1065,17 @@ hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t
 hipError_t launch_layernorm(float* out, const float* in, const float* gamma, const float* beta,
                             int M, int N, float eps, hipStream_t s) {
     if (M == 0) return hipSuccess;
+    if (split_rows(M, N)) {
+        return launch_split(M, N, rows_vec4(N, {out, in, gamma, beta}), true, in, s,
+                            [&](bool vec, dim3 grid, int nseg, const float* p1, const float* p2) {
+                                if (vec)
+                                    hipLaunchKernelGGL(layernorm_seg_write_kernel<true>, grid, dim3(ST), 0,
+                                                       s, out, in, gamma, beta, N, eps, nseg, p1, p2);
+                                else
+                                    hipLaunchKernelGGL(layernorm_seg_write_kernel<false>, grid, dim3(ST), 0,
+                                                       s, out, in, gamma, beta, N, eps, nseg, p1, p2);
+                            });
+    }
     if (N > MAX_BLOCK_CACHED) {
         if (rows_vec4(N, {out, in, gamma, beta}))
             hipLaunchKernelGGL(layernorm_long_kernel<true>, dim3(M), dim3(BT), HEAD_LDS, s, out, in, gamma,
@@ -879,7 +1098,19 @@ hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, flo
                                 float* loss, float* row_loss, int M, int N, hipStream_t s) {
     hipError_t e = hipSuccess;
     if (M > 0) {
-        if (N > MAX_BLOCK_CACHED) {
+        if (split_rows(M, N)) {
+            e = launch_split(M, N, rows_vec4(N, {logits, grad}), false, logits, s,
+                             [&](bool vec, dim3 grid, int nseg, const float* p1, const float* p2) {
+                                 if (vec)
+                                     hipLaunchKernelGGL(cross_entropy_seg_write_kernel<true>, grid, dim3(ST),
+                                                        0, s, logits, targets, grad, row_loss, M, N, nseg,
+                                                        p1, p2);
+                                 else
+                                     hipLaunchKernelGGL(cross_entropy_seg_write_kernel<false>, grid, dim3(ST),
+                                                        0, s, logits, targets, grad, row_loss, M, N, nseg,
+                                                        p1, p2);
+                             });
+        } else if (N > MAX_BLOCK_CACHED) {
             if (rows_vec4(N, {logits, grad}))
                 hipLaunchKernelGGL(cross_entropy_long_kernel<true>, dim3(M), dim3(BT), HEAD_LDS, s, logits,
                                    targets, grad, row_loss, M, N);

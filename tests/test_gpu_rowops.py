@@ -11,7 +11,10 @@ layernorm [64,256], [2048,256]), the 16-element vector/tail split (N = 15,
 rows of 4097-65536 held by one 1024-thread block (16-byte and 4-byte
 accesses, with and without a tail), rows longer than 65536 (the streaming
 passes, 16-byte and 4-byte accesses, up to 131073), rows that are not
-16-byte aligned (the 4-byte path) and in-place softmax and cross entropy."""
+16-byte aligned (the 4-byte path) and in-place softmax and cross entropy.
+Up to 64 rows longer than 65536 are split over 4096-element segments (three
+launches); the shapes with 65 rows keep the one-workgroup-per-row streaming
+path covered."""
 import numpy as np
 import pytest
 import torch
@@ -26,7 +29,9 @@ pytestmark = pytest.mark.gpu
 SHAPES = [(64, 256), (64, 10), (2048, 2048), (2048, 256), (1, 1), (3, 15), (5, 16), (7, 17),
           (9, 33), (13, 100), (6, 600), (5, 1500), (3, 4000), (3, 4096), (2, 4097), (2, 10000),
           (3, 16386), (2, 20001), (2, 32768), (2, 32769), (2, 40000), (2, 50257), (2, 65536),
-          (2, 65537), (1, 131073)]
+          (2, 65537), (1, 131073),
+          # more rows than the split path takes (64): one streaming workgroup per row
+          (65, 70001)]
 
 
 def _x(M, N, seed, scale=3.0):
@@ -138,7 +143,7 @@ def test_layernorm_epsilon_and_constant_rows(dev):
 
 @pytest.mark.parametrize("M,N", [(64, 10), (128, 1000), (7, 17), (1, 1), (5, 4096), (3, 7000),
                                  (2048, 512), (3, 32000), (2, 20001), (2, 40000), (2, 50257),
-                                 (2, 65537), (2, 131072)])
+                                 (2, 65537), (2, 131072), (65, 131072)])
 def test_cross_entropy(dev, M, N):
     case(f"cross entropy [{M},{N}]")
     x = _x(M, N, 3 * M + N)
@@ -191,12 +196,13 @@ def test_cross_entropy_bad_target_and_repeat(dev):
     np.testing.assert_allclose(to_np(g2)[2], po.softmax(x)[2] / 6, rtol=2e-6)
 
 
-@pytest.mark.parametrize("N", [256, 2048, 8192, 40000, 70000])
-def test_unaligned_rows_and_in_place(dev, N):
+@pytest.mark.parametrize("M,N", [(5, 256), (5, 2048), (5, 8192), (5, 40000), (5, 70000),
+                                 (65, 40000), (65, 70000)])
+def test_unaligned_rows_and_in_place(dev, M, N):
     """Rows whose start is only 4-byte aligned take the 4-byte path (same
-    results); cross entropy with grad written over the logits."""
-    case(f"row kernels unaligned, in place N={N}")
-    M = 5
+    results); cross entropy with grad written over the logits.  Five rows of
+    70000 take the split path, 65 the streaming one."""
+    case(f"row kernels unaligned, in place [{M},{N}]")
     x = _x(M, N, N + 1)
     flat = torch.empty((M * N + 1,), dtype=torch.float32, device=dev)
     xs = flat[1:].view(M, N)
@@ -217,6 +223,38 @@ def test_unaligned_rows_and_in_place(dev, N):
     xa = to_dev(x, torch.float32, dev)
     loss, gg = ops.cross_entropy(xa, to_dev(t, torch.int32, dev), grad=xa)  # in place, aligned
     _check_cross_entropy(float(to_np(loss)[0]), to_np(gg), x, t)
+
+
+@pytest.mark.parametrize("N", [70000, 70003])
+def test_split_rows_segment_edges(dev, N):
+    """Few long rows are split over workgroups of 4096-element segments
+    (16-byte accesses at N = 70000, 4-byte with a tail at 70003): the targets
+    sit on both sides of a segment edge and at the row's end, one row has an
+    invalid target (NaN loss, no onehot subtraction), and the cross entropy
+    runs in place."""
+    case(f"split rows, segment edges N={N}")
+    M = 4
+    x = _x(M, N, 77)
+    t = np.array([4095, 4096, N - 1, N], np.int32)  # the last one is invalid
+    xt = to_dev(x, torch.float32, dev)
+    _check_softmax(to_np(ops.softmax(xt)), x)
+    gam = np.linspace(-1, 1, N).astype(np.float32)
+    bet = np.linspace(2, 0, N).astype(np.float32)
+    y = to_np(ops.layernorm(xt, to_dev(gam, torch.float32, dev), to_dev(bet, torch.float32, dev)))
+    assert I.rel_err(y, po.layernorm64(x, gam, bet)) < I.TOL["f32"]
+    assert I.rel_err(y, po.layernorm(x, gam, bet)) < 2e-6
+    loss, g = ops.cross_entropy(xt, to_dev(t, torch.int32, dev), grad=xt)  # in place
+    assert np.isnan(float(to_np(loss)[0]))
+    g = to_np(g)
+    # (p - onehot) / M, the invalid row without the onehot
+    p = _exact_sum(po.softmax(x))
+    gx = p / M
+    rows = np.arange(3)
+    gx[rows, t[:3]] -= 1.0 / M
+    off = np.ones_like(gx, bool)
+    off[rows, t[:3]] = False
+    assert _ratio_err(np.where(off, g, 0.0), np.where(off, gx, 0.0)) < 1e-6
+    assert np.max(np.abs(g[rows, t[:3]] - gx[rows, t[:3]])) <= 1e-6 / M
 
 
 def test_registry_row_kernels(dev):
