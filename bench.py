@@ -10,7 +10,7 @@ synthetic inputs.  `value` is their combined algorithmic TFLOP/s
 The same run also times every BASELINE config on its own (per_config, keys
 c1-c5; c5p is C5 on the packed weight layout), the reference's published shapes (per_config, keys
 g1-g3: fp32 matmuls, a1: fp32 non-causal flash attention; each beside its published time and the
-ratio to it), the row kernels (per_config, keys r1-r8: softmax, layernorm, cross
+ratio to it), the row kernels (per_config, keys r1-r9: softmax, layernorm, cross
 entropy, GB/s against HBM), the 2-layer MLP forward + loss + backward
 (per_config, keys m1-m2, fp32 TFLOP/s), the flash-attention backward at C4's
 shape (per_config, key b4), matmulInt8 (per_config, keys i1-i2: int8 TOP/s at
@@ -78,7 +78,9 @@ PACKED_CONFIGS = {
 # and one large shape each, where launch latency does not dominate; then the
 # cross entropy of a language-model head at two vocabulary sizes: 50257 (a
 # row held at 64 elements per thread, 4-byte accesses, a tail) and 128256
-# (rows streamed in three passes).
+# (the first 65536 elements held, the rest streamed in three passes); and a
+# decode-sized softmax over that vocabulary (8 rows, each split over
+# workgroups).
 ROW_CONFIGS = {
     "r1": dict(kind="softmax", M=2048, N=2048),
     "r2": dict(kind="softmax", M=16384, N=4096),
@@ -88,6 +90,7 @@ ROW_CONFIGS = {
     "r6": dict(kind="xent", M=4096, N=32000),
     "r7": dict(kind="xent", M=2048, N=50257),
     "r8": dict(kind="xent", M=512, N=128256),
+    "r9": dict(kind="softmax", M=8, N=128256),
 }
 
 
@@ -695,7 +698,7 @@ def main():
     ap.add_argument("--pmc", action="store_true",
                     help="counter-collection workload for rocprofv3 --pmc: one 64 MiB device "
                          "copy of known size (calibration), 3 MFMA calibration launches, then 3 "
-                         "launches of C3, C4 and C5")
+                         "launches each of C3, C4, C5, C5 packed and the row configs r6-r9")
     ap.add_argument("--vendor", action="store_true",
                     help="time the vendor library on C3's GEMM for comparison: torch.mm in bf16 "
                          "at 4096^3 (hipBLASLt; GEMM only, no bias or GELU) beside this build's C3 "
@@ -749,8 +752,8 @@ def main():
             c.launch()  # MFMA calibration dispatches (clock and MFMA busy under load)
         torch.cuda.synchronize()
         del c
-        for name in ("c3", "c4", "c5", "c5p"):
-            r = Runner(name, {**CONFIGS, **PACKED_CONFIGS}[name], dev)
+        for name in ("c3", "c4", "c5", "c5p", "r6", "r7", "r8", "r9"):
+            r = Runner(name, {**CONFIGS, **PACKED_CONFIGS, **ROW_CONFIGS}[name], dev)
             for _ in range(3):
                 r.launch()
             torch.cuda.synchronize()
