@@ -1034,7 +1034,7 @@ hipError_t launch_split(int M, int N, bool vec, bool layer, const float* x, hipS
 }  // namespace
 
 hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t s) {
-    if (M == 0) return hipSuccess;
+    if (M <= 0 || N <= 0) return hipSuccess;  // no rows, or rows with nothing to load
     if (split_rows(M, N)) {
         return launch_split(M, N, rows_vec4(N, {out, in}), false, in, s,
                             [&](bool vec, dim3 grid, int nseg, const float* p1, const float* p2) {
@@ -1064,7 +1064,7 @@ hipError_t launch_softmax(float* out, const float* in, int M, int N, hipStream_t
 
 hipError_t launch_layernorm(float* out, const float* in, const float* gamma, const float* beta,
                             int M, int N, float eps, hipStream_t s) {
-    if (M == 0) return hipSuccess;
+    if (M <= 0 || N <= 0) return hipSuccess;
     if (split_rows(M, N)) {
         return launch_split(M, N, rows_vec4(N, {out, in, gamma, beta}), true, in, s,
                             [&](bool vec, dim3 grid, int nseg, const float* p1, const float* p2) {
@@ -1097,6 +1097,7 @@ hipError_t launch_layernorm(float* out, const float* in, const float* gamma, con
 hipError_t launch_cross_entropy(const float* logits, const int32_t* targets, float* grad,
                                 float* loss, float* row_loss, int M, int N, hipStream_t s) {
     hipError_t e = hipSuccess;
+    if (M > 0 && N <= 0) return hipErrorInvalidValue;  // a target has no row to index
     if (M > 0) {
         if (split_rows(M, N)) {
             e = launch_split(M, N, rows_vec4(N, {logits, grad}), false, logits, s,
