@@ -194,10 +194,30 @@ __global__ __launch_bounds__(64 * RWV) void gemm_f32_rowsdma_kernel(
     const int mb = blockIdx.y * RW * RWV;
     const int nst = (K + RD_KG - 1) / RD_KG;
 
-    // stage rows mb .. mb + RW*RWV - 1 of A (rows past M repeat row M-1)
-    for (int i = threadIdx.x; i < RW * RWV * K; i += 64 * RWV) {
-        const int r = i / K, k = i - r * K;
-        sA[r * Kp + k] = A[(int64_t)min(mb + r, M - 1) * K + k];
+    // stage rows mb .. mb + RW*RWV - 1 of A (rows past M repeat row M-1):
+    // the rows unrolled, so a thread's loads of all of them are in flight
+    // together (one load, its wait and its LDS store at a time took a memory
+    // latency per element), 16-byte pieces when every row is 16-byte aligned
+    constexpr int AR = RW * RWV;
+    const float* arow[AR];
+#pragma unroll
+    for (int r = 0; r < AR; ++r) arow[r] = A + (int64_t)min(mb + r, M - 1) * K;
+    if ((K & 3) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0) {
+        for (int c = threadIdx.x; 4 * c < K; c += 64 * RWV) {
+            f32x4_t v[AR];
+#pragma unroll
+            for (int r = 0; r < AR; ++r) v[r] = *reinterpret_cast<const f32x4_t*>(arow[r] + 4 * c);
+#pragma unroll
+            for (int r = 0; r < AR; ++r) *reinterpret_cast<f32x4_t*>(sA + r * Kp + 4 * c) = v[r];
+        }
+    } else {
+        for (int k = threadIdx.x; k < K; k += 64 * RWV) {
+            float v[AR];
+#pragma unroll
+            for (int r = 0; r < AR; ++r) v[r] = arow[r][k];
+#pragma unroll
+            for (int r = 0; r < AR; ++r) sA[r * Kp + k] = v[r];
+        }
     }
     __syncthreads();
 
