@@ -332,7 +332,7 @@ __device__ __forceinline__ int held_row(int* tid) {
 
 template <int G, int ELEMS, bool VEC, bool FULL>
 __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void softmax_kernel(
-    float* __restrict__ out, const float* __restrict__ in, int M, int N) {
+    float* out, const float* in, int M, int N) {  // out may alias in
     __shared__ float red[G == 64 ? 1 : G / 64];
     int tid;
     const int row = held_row<G>(&tid);
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(BT) void softmax_long_kernel(float* out, const floa
 // ---- layernorm ----
 template <int G, int ELEMS, bool VEC, bool FULL>
 __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void layernorm_kernel(
-    float* __restrict__ out, const float* __restrict__ in, const float* __restrict__ gamma,
+    float* out, const float* in, const float* __restrict__ gamma,  // out may alias in
     const float* __restrict__ beta, int M, int N, float eps) {
     __shared__ float red[G == 64 ? 1 : G / 64];
     int tid;
@@ -658,8 +658,8 @@ __global__ __launch_bounds__(BT) void layernorm_long_kernel(float* out, const fl
 // same thread's later store to the same address wins).
 template <int G, int ELEMS, bool VEC, bool FULL>
 __global__ __launch_bounds__(G == 64 ? 64 * ROWS_PER_BLOCK : BT) void cross_entropy_kernel(
-    const float* __restrict__ logits, const int32_t* __restrict__ targets,
-    float* __restrict__ grad, float* __restrict__ row_loss, int M, int N) {
+    const float* logits, const int32_t* __restrict__ targets,  // grad may alias logits
+    float* grad, float* __restrict__ row_loss, int M, int N) {
     __shared__ float red[G == 64 ? 1 : G / 64];
     int tid;
     const int row = held_row<G>(&tid);
