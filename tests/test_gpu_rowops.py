@@ -30,8 +30,9 @@ SHAPES = [(64, 256), (64, 10), (2048, 2048), (2048, 256), (1, 1), (3, 15), (5, 1
           (9, 33), (13, 100), (6, 600), (5, 1500), (3, 4000), (3, 4096), (2, 4097), (2, 10000),
           (3, 16386), (2, 20001), (2, 32768), (2, 32769), (2, 40000), (2, 50257), (2, 65536),
           (2, 65537), (1, 131073),
-          # more rows than the split path takes (64): one streaming workgroup per row
-          (65, 70001)]
+          # the most rows the split path takes (64), and one more: one streaming
+          # workgroup per row
+          (64, 65537), (65, 70001)]
 
 
 def _x(M, N, seed, scale=3.0):
@@ -143,7 +144,7 @@ def test_layernorm_epsilon_and_constant_rows(dev):
 
 @pytest.mark.parametrize("M,N", [(64, 10), (128, 1000), (7, 17), (1, 1), (5, 4096), (3, 7000),
                                  (2048, 512), (3, 32000), (2, 20001), (2, 40000), (2, 50257),
-                                 (2, 65537), (2, 131072), (65, 131072)])
+                                 (2, 65537), (2, 131072), (64, 65540), (65, 131072)])
 def test_cross_entropy(dev, M, N):
     case(f"cross entropy [{M},{N}]")
     x = _x(M, N, 3 * M + N)
